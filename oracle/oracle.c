@@ -1,0 +1,561 @@
+/*
+ * oracle.c — CPU restatement of the SeedVR2 AWA path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP implementation.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it; the
+ * product (seedvr2-2b-ncnn_amd/) never does.
+ *
+ * Built like the reference (CMakeLists.txt:50): -O2, x86-64 baseline ISA (no
+ * FMA instructions exist, so nothing can be contracted), -ffp-contract=off,
+ * no -ffast-math.  Each function keeps the reference's float operation order.
+ *
+ * How each function is pinned (tests/test_oracle_*.py):
+ *   orc_make_windows   window counts, S ranges, sum S and example split points
+ *                      produced by the reference's own awa_window.cpp
+ *                      (tests/golden/window_summary.json); closed-form integer
+ *                      restatement; tiling invariant (every token exactly once).
+ *   orc_build_freqs    FNV-1a hashes of the reference's tables
+ *                      (tests/golden/window_summary.json); closed form per
+ *                      channel; pair-repetition invariant.
+ *   orc_build_index    tiling invariant + brute-force membership.
+ *   orc_qk_norm, orc_apply_rope, orc_rmsnorm, orc_sinusoidal, orc_silu,
+ *   orc_linear         bit-exact against the reference's own static functions
+ *                      (src/verify_dit.cpp) compiled into oracle/_ref; closed
+ *                      forms (unit-norm output, rotation preserves pair norms).
+ *   orc_awa_forward    bit-exact against verify_dit.cpp::awa_forward compiled
+ *                      into oracle/_ref (identity out-projection); fp64 SDPA
+ *                      special case (one window = plain attention).
+ *   orc_f32_to_bf16    table of hand-checked cases (ties to even, carries into
+ *                      the exponent, signed zero).
+ *   orc_dit_layer      composed of the functions above in dit_vk.cpp:517-632
+ *                      order; bit-exact against the same loop written over
+ *                      the reference's own functions in oracle/_ref.
+ *   orc_time_embedding bit-exact against verify_dit.cpp::time_embedding.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define HEADS ORC_HEADS
+#define HEAD_D ORC_HEAD_D
+#define DIM ORC_DIM
+#define QKV ORC_QKV
+#define ROPE_ROT ORC_ROPE_ROT
+
+static int imin(int a, int b) { return a < b ? a : b; }
+static int imax(int a, int b) { return a > b ? a : b; }
+
+/* ------------------------------------------------------------------------ */
+/* Window geometry — src/awa_window.cpp:15-78                               */
+/* ------------------------------------------------------------------------ */
+
+static void push_win(int32_t* slices, int cap, int* n, int a, int b, int c,
+                     int d, int e, int f) {
+    if (*n < cap) {
+        int32_t* s = slices + (size_t)(*n) * 6;
+        s[0] = a; s[1] = b; s[2] = c; s[3] = d; s[4] = e; s[5] = f;
+    }
+    (*n)++;
+}
+
+int orc_make_windows(int t, int h, int w, const int num_windows[3], int shifted,
+                     int32_t* slices, int cap) {
+    int rnt = num_windows[0], rnh = num_windows[1], rnw = num_windows[2];
+    /* awa_window.cpp:21-26 */
+    double scale = sqrt((45.0 * 80.0) / ((double)h * w));
+    int resized_h = (int)round(h * scale);
+    int resized_w = (int)round(w * scale);
+    int wh = (resized_h + rnh - 1) / rnh;
+    int ww = (resized_w + rnw - 1) / rnw;
+    int wt = (imin(t, 30) + rnt - 1) / rnt;
+    int n = 0;
+    if (!shifted) {
+        /* awa_window.cpp:27-39: loops iw -> ih -> it, empty windows skipped */
+        int nt = (t + wt - 1) / wt, nh = (h + wh - 1) / wh, nw = (w + ww - 1) / ww;
+        for (int iw = 0; iw < nw; iw++)
+            if (imin((iw + 1) * ww, w) > iw * ww)
+                for (int ih = 0; ih < nh; ih++)
+                    if (imin((ih + 1) * wh, h) > ih * wh)
+                        for (int it = 0; it < nt; it++)
+                            if (imin((it + 1) * wt, t) > it * wt)
+                                push_win(slices, cap, &n, it * wt, imin((it + 1) * wt, t),
+                                         ih * wh, imin((ih + 1) * wh, h),
+                                         iw * ww, imin((iw + 1) * ww, w));
+        return n;
+    }
+    /* awa_window.cpp:52-77: half-window shift where the window is smaller
+     * than the axis; int() truncates toward zero. */
+    double st = (wt < t) ? 0.5 : 0.0;
+    double sh = (wh < h) ? 0.5 : 0.0;
+    double sw = (ww < w) ? 0.5 : 0.0;
+    int nt = (int)ceil((t - st) / wt);
+    int nh = (int)ceil((h - sh) / wh);
+    int nw = (int)ceil((w - sw) / ww);
+    nt = (st > 0) ? nt + 1 : 1;
+    nh = (sh > 0) ? nh + 1 : 1;
+    nw = (sw > 0) ? nw + 1 : 1;
+    for (int iw = 0; iw < nw; iw++)
+        if (imin((int)((iw - sw + 1) * ww), w) > imax((int)((iw - sw) * ww), 0))
+            for (int ih = 0; ih < nh; ih++)
+                if (imin((int)((ih - sh + 1) * wh), h) > imax((int)((ih - sh) * wh), 0))
+                    for (int it = 0; it < nt; it++)
+                        if (imin((int)((it - st + 1) * wt), t) > imax((int)((it - st) * wt), 0))
+                            push_win(slices, cap, &n,
+                                     imax((int)((it - st) * wt), 0), imin((int)((it - st + 1) * wt), t),
+                                     imax((int)((ih - sh) * wh), 0), imin((int)((ih - sh + 1) * wh), h),
+                                     imax((int)((iw - sw) * ww), 0), imin((int)((iw - sw + 1) * ww), w));
+    return n;
+}
+
+/* src/awa_window.cpp:81-131: window-local (TXT+it, ih, iw) positions for
+ * video rows, 1-D positions tiled over the three axes for text rows; the
+ * products are formed in double and rounded once to float. */
+int orc_build_freqs(const int32_t* slices, int nwin, int txt_len,
+                    float* vid_freq, float* txt_freq) {
+    const int ROT = 42;
+    double base[21];
+    for (int j = 0; j < 21; j++) base[j] = 1.0 / pow(10000.0, (double)(j * 2) / 42);
+    size_t off = 0;
+    int total = 0;
+    for (int i = 0; i < nwin; i++) {
+        const int32_t* s = slices + (size_t)i * 6;
+        int wt = s[1] - s[0], wh = s[3] - s[2], ww = s[5] - s[4];
+        total += wt * wh * ww;
+        for (int it = 0; it < wt; it++) {
+            int tt = txt_len + it;
+            for (int ih = 0; ih < wh; ih++)
+                for (int iw = 0; iw < ww; iw++)
+                    for (int k = 0; k < ROPE_ROT; k++) {
+                        double v;
+                        if (k < ROT) v = (double)tt * base[k / 2];
+                        else if (k < 2 * ROT) v = (double)ih * base[(k - ROT) / 2];
+                        else v = (double)iw * base[(k - 2 * ROT) / 2];
+                        if (vid_freq) vid_freq[off] = (float)v;
+                        off++;
+                    }
+        }
+    }
+    if (txt_freq) {
+        off = 0;
+        for (int i = 0; i < nwin; i++)
+            for (int it = 0; it < txt_len; it++)
+                for (int k = 0; k < ROPE_ROT; k++) {
+                    int kk = k % ROT;
+                    txt_freq[off++] = (float)((double)it * base[kk / 2]);
+                }
+    }
+    return total;
+}
+
+/* src/awa_vk.cpp:73-88: cumf prefix of window sizes; vidx lists the grid
+ * token of every window row, window-major then t, h, w in C order. */
+int orc_build_index(const int32_t* slices, int nwin, int H, int W,
+                    int32_t* cumf, int32_t* vidx) {
+    cumf[0] = 0;
+    int g = 0;
+    for (int wi = 0; wi < nwin; wi++) {
+        const int32_t* s = slices + (size_t)wi * 6;
+        cumf[wi + 1] = cumf[wi] + (s[1] - s[0]) * (s[3] - s[2]) * (s[5] - s[4]);
+        for (int lt = s[0]; lt < s[1]; lt++)
+            for (int lh = s[2]; lh < s[3]; lh++)
+                for (int lw = s[4]; lw < s[5]; lw++) vidx[g++] = ((lt * H) + lh) * W + lw;
+    }
+    return g;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Per-token ops — src/dit_vk.cpp:48-71                                     */
+/* ------------------------------------------------------------------------ */
+
+void orc_rmsnorm(const float* x, int n, const float* w, float eps, float* out) {
+    double s = 0;
+    for (int i = 0; i < n; i++) s += (double)x[i] * x[i];
+    float r = 1.0f / sqrtf((float)(s / n) + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * r * (w ? w[i] : 1.f);
+}
+
+void orc_qk_norm(const float* x, const float* w, float eps, float* out) {
+    for (int h = 0; h < HEADS; h++) {
+        const float* xp = x + h * HEAD_D;
+        float* op = out + h * HEAD_D;
+        float sq = 0;
+        for (int d = 0; d < HEAD_D; d++) sq += xp[d] * xp[d];
+        float r = sqrtf(sq / HEAD_D + eps);
+        for (int d = 0; d < HEAD_D; d++) op[d] = xp[d] / r * w[d];
+    }
+}
+
+void orc_apply_rope(const float* freq, const float* q, float* out) {
+    /* adjacent pairs (2i, 2i+1) rotate together; channels 126, 127 pass */
+    for (int k = 0; k < ROPE_ROT; k++) {
+        float c = cosf(freq[k]), s = sinf(freq[k]);
+        float rh = (k % 2 == 0) ? -q[k + 1] : q[k - 1];
+        out[k] = q[k] * c + rh * s;
+    }
+    for (int k = ROPE_ROT; k < HEAD_D; k++) out[k] = q[k];
+}
+
+/* ------------------------------------------------------------------------ */
+/* The AWA op — src/dit_vk.cpp:345-462                                      */
+/* ------------------------------------------------------------------------ */
+
+void orc_awa_forward(const float* vqkv, const float* tqkv, int Lv, int TXT,
+                     int T, int H, int W, const int32_t* slices, int nwin,
+                     const float* vid_freq, const float* txt_freq,
+                     const float* nq_v, const float* nk_v,
+                     const float* nq_t, const float* nk_t, float eps,
+                     float* vattn, float* tattn, int nthreads) {
+    (void)T;
+    size_t LD = (size_t)DIM;
+    float* vq = (float*)malloc(sizeof(float) * Lv * LD);
+    float* vk = (float*)malloc(sizeof(float) * Lv * LD);
+    float* vv = (float*)malloc(sizeof(float) * Lv * LD);
+    float* tq = (float*)malloc(sizeof(float) * (TXT > 0 ? TXT : 1) * LD);
+    float* tk = (float*)malloc(sizeof(float) * (TXT > 0 ? TXT : 1) * LD);
+    float* tv = (float*)malloc(sizeof(float) * (TXT > 0 ? TXT : 1) * LD);
+    /* dit_vk.cpp:348-361 */
+    for (int ii = 0; ii < Lv; ii++) {
+        const float* q = vqkv + (size_t)ii * QKV;
+        orc_qk_norm(q, nq_v, eps, vq + ii * LD);
+        orc_qk_norm(q + 2560, nk_v, eps, vk + ii * LD);
+        memcpy(vv + ii * LD, q + 5120, DIM * 4);
+    }
+    for (int ii = 0; ii < TXT; ii++) {
+        const float* q = tqkv + (size_t)ii * QKV;
+        orc_qk_norm(q, nq_t, eps, tq + ii * LD);
+        orc_qk_norm(q + 2560, nk_t, eps, tk + ii * LD);
+        memcpy(tv + ii * LD, q + 5120, DIM * 4);
+    }
+    /* dit_vk.cpp:362-381: cumf and video partition */
+    int32_t* cumf = (int32_t*)malloc(sizeof(int32_t) * (nwin + 1));
+    cumf[0] = 0;
+    for (int wi = 0; wi < nwin; wi++) {
+        const int32_t* s = slices + wi * 6;
+        cumf[wi + 1] = cumf[wi] + (s[1] - s[0]) * (s[3] - s[2]) * (s[5] - s[4]);
+    }
+    int sumf = cumf[nwin];
+    float* vqw = (float*)malloc(sizeof(float) * (size_t)(sumf > 0 ? sumf : 1) * LD);
+    float* vkw = (float*)malloc(sizeof(float) * (size_t)(sumf > 0 ? sumf : 1) * LD);
+    float* vvw = (float*)malloc(sizeof(float) * (size_t)(sumf > 0 ? sumf : 1) * LD);
+    for (int wi = 0; wi < nwin; wi++) {
+        const int32_t* s = slices + wi * 6;
+        int local = 0;
+        for (int lt = s[0]; lt < s[1]; lt++)
+            for (int lh = s[2]; lh < s[3]; lh++)
+                for (int lw = s[4]; lw < s[5]; lw++) {
+                    size_t idx = (size_t)(((lt * H) + lh) * W + lw);
+                    size_t dst = (size_t)(cumf[wi] + local);
+                    memcpy(vqw + dst * LD, vq + idx * LD, DIM * 4);
+                    memcpy(vkw + dst * LD, vk + idx * LD, DIM * 4);
+                    memcpy(vvw + dst * LD, vv + idx * LD, DIM * 4);
+                    local++;
+                }
+    }
+    /* dit_vk.cpp:382-390: RoPE on partitioned video rows */
+    for (int dst = 0; dst < sumf; dst++) {
+        const float* fr = vid_freq + (size_t)dst * ROPE_ROT;
+        for (int hh = 0; hh < HEADS; hh++) {
+            float inb[HEAD_D], outb[HEAD_D];
+            memcpy(inb, vqw + dst * LD + hh * HEAD_D, HEAD_D * 4);
+            orc_apply_rope(fr, inb, outb);
+            memcpy(vqw + dst * LD + hh * HEAD_D, outb, HEAD_D * 4);
+            memcpy(inb, vkw + dst * LD + hh * HEAD_D, HEAD_D * 4);
+            orc_apply_rope(fr, inb, outb);
+            memcpy(vkw + dst * LD + hh * HEAD_D, outb, HEAD_D * 4);
+        }
+    }
+    /* dit_vk.cpp:391-405: text tiled per window, RoPE'd with that window's rows */
+    size_t ntw = (size_t)nwin * TXT;
+    float* tqw = (float*)malloc(sizeof(float) * (ntw > 0 ? ntw : 1) * LD);
+    float* tkw = (float*)malloc(sizeof(float) * (ntw > 0 ? ntw : 1) * LD);
+    float* tvw = (float*)malloc(sizeof(float) * (ntw > 0 ? ntw : 1) * LD);
+    for (int wi = 0; wi < nwin; wi++)
+        for (int ii = 0; ii < TXT; ii++) {
+            size_t dst = (size_t)wi * TXT + ii;
+            memcpy(tqw + dst * LD, tq + ii * LD, DIM * 4);
+            memcpy(tkw + dst * LD, tk + ii * LD, DIM * 4);
+            memcpy(tvw + dst * LD, tv + ii * LD, DIM * 4);
+            const float* fr = txt_freq + dst * ROPE_ROT;
+            for (int hh = 0; hh < HEADS; hh++) {
+                float inb[HEAD_D], outb[HEAD_D];
+                memcpy(inb, tqw + dst * LD + hh * HEAD_D, HEAD_D * 4);
+                orc_apply_rope(fr, inb, outb);
+                memcpy(tqw + dst * LD + hh * HEAD_D, outb, HEAD_D * 4);
+                memcpy(inb, tkw + dst * LD + hh * HEAD_D, HEAD_D * 4);
+                orc_apply_rope(fr, inb, outb);
+                memcpy(tkw + dst * LD + hh * HEAD_D, outb, HEAD_D * 4);
+            }
+        }
+    /* dit_vk.cpp:406-439: per (window, head) SDPA over S = f + TXT rows with
+     * one max over the whole S x S score block, expf, divide-then-accumulate */
+    float* vout_win = (float*)calloc((size_t)(sumf > 0 ? sumf : 1) * LD, sizeof(float));
+    float* tout_win = (float*)calloc((ntw > 0 ? ntw : 1) * LD, sizeof(float));
+    float scale = 1.0f / sqrtf((float)HEAD_D);
+    int npairs = nwin * HEADS;
+#ifdef _OPENMP
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+#endif
+    for (int pi = 0; pi < npairs; pi++) {
+        int wi = pi / HEADS, hh = pi % HEADS;
+        int f_i = cumf[wi + 1] - cumf[wi];
+        int S = f_i + TXT;
+        float* qseg = (float*)malloc(sizeof(float) * (size_t)S * HEAD_D);
+        float* kseg = (float*)malloc(sizeof(float) * (size_t)S * HEAD_D);
+        float* vseg = (float*)malloc(sizeof(float) * (size_t)S * HEAD_D);
+        float* sc = (float*)malloc(sizeof(float) * (size_t)S * S);
+        float* p = (float*)malloc(sizeof(float) * (size_t)S);
+        for (int j = 0; j < f_i; j++) {
+            size_t src = (size_t)(cumf[wi] + j) * LD + hh * HEAD_D;
+            memcpy(qseg + j * HEAD_D, vqw + src, HEAD_D * 4);
+            memcpy(kseg + j * HEAD_D, vkw + src, HEAD_D * 4);
+            memcpy(vseg + j * HEAD_D, vvw + src, HEAD_D * 4);
+        }
+        for (int ii = 0; ii < TXT; ii++) {
+            int s = f_i + ii;
+            size_t src = ((size_t)wi * TXT + ii) * LD + hh * HEAD_D;
+            memcpy(qseg + s * HEAD_D, tqw + src, HEAD_D * 4);
+            memcpy(kseg + s * HEAD_D, tkw + src, HEAD_D * 4);
+            memcpy(vseg + s * HEAD_D, tvw + src, HEAD_D * 4);
+        }
+        float mx = -1e30f;
+        for (int a = 0; a < S; a++) {
+            const float* qa = qseg + a * HEAD_D;
+            for (int b = 0; b < S; b++) {
+                const float* kb = kseg + b * HEAD_D;
+                float dot = 0;
+                for (int d = 0; d < HEAD_D; d++) dot += qa[d] * kb[d];
+                dot *= scale;
+                sc[(size_t)a * S + b] = dot;
+                if (dot > mx) mx = dot;
+            }
+        }
+        for (int a = 0; a < S; a++) {
+            float sm = 0;
+            for (int b = 0; b < S; b++) {
+                float e = expf(sc[(size_t)a * S + b] - mx);
+                p[b] = e;
+                sm += e;
+            }
+            for (int b = 0; b < S; b++) p[b] /= sm;
+            float o[HEAD_D];
+            for (int d = 0; d < HEAD_D; d++) o[d] = 0.f;
+            for (int b = 0; b < S; b++) {
+                const float* vb = vseg + b * HEAD_D;
+                for (int d = 0; d < HEAD_D; d++) o[d] += p[b] * vb[d];
+            }
+            if (a < f_i)
+                memcpy(vout_win + (size_t)(cumf[wi] + a) * LD + hh * HEAD_D, o, HEAD_D * 4);
+            else
+                memcpy(tout_win + ((size_t)wi * TXT + (a - f_i)) * LD + hh * HEAD_D, o, HEAD_D * 4);
+        }
+        free(qseg); free(kseg); free(vseg); free(sc); free(p);
+    }
+    /* dit_vk.cpp:440-444: text average in window order */
+    for (size_t i = 0; i < (size_t)TXT * LD; i++) tattn[i] = 0.f;
+    for (int wi = 0; wi < nwin; wi++)
+        for (int ii = 0; ii < TXT; ii++)
+            for (int d = 0; d < DIM; d++)
+                tattn[(size_t)ii * LD + d] += tout_win[((size_t)wi * TXT + ii) * LD + d];
+    for (size_t i = 0; i < (size_t)TXT * LD; i++) tattn[i] /= (float)nwin;
+    /* dit_vk.cpp:445-455: reverse partition, uncovered tokens stay zero */
+    memset(vattn, 0, sizeof(float) * (size_t)Lv * LD);
+    for (int wi = 0; wi < nwin; wi++) {
+        const int32_t* s = slices + wi * 6;
+        int local = 0;
+        for (int lt = s[0]; lt < s[1]; lt++)
+            for (int lh = s[2]; lh < s[3]; lh++)
+                for (int lw = s[4]; lw < s[5]; lw++) {
+                    size_t idx = (size_t)(((lt * H) + lh) * W + lw);
+                    memcpy(vattn + idx * LD, vout_win + (size_t)(cumf[wi] + local) * LD, DIM * 4);
+                    local++;
+                }
+    }
+    free(vq); free(vk); free(vv); free(tq); free(tk); free(tv); free(cumf);
+    free(vqw); free(vkw); free(vvw); free(tqw); free(tkw); free(tvw);
+    free(vout_win); free(tout_win);
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16 boundary — shaders/cast_f32_bf16.comp:23-24, cast_bf16_f32.comp:18-19 */
+/* ------------------------------------------------------------------------ */
+
+void orc_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t u;
+        memcpy(&u, in + i, 4);
+        out[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    }
+}
+
+void orc_bf16_to_f32(const uint16_t* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t u = (uint32_t)in[i] << 16;
+        memcpy(out + i, &u, 4);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Block surroundings                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* LinearRaw::run (verify_dit.cpp:59-72) */
+void orc_linear(const float* x, const float* W, const float* b, int Ln, int in,
+                int out, float* y, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int t = 0; t < Ln; t++) {
+        const float* xi = x + (size_t)t * in;
+        float* yo = y + (size_t)t * out;
+        for (int o = 0; o < out; o++) {
+            const float* wi = W + (size_t)o * in;
+            float acc = 0.f;
+            for (int i = 0; i < in; i++) acc += xi[i] * wi[i];
+            yo[o] = acc + (b ? b[o] : 0.f);
+        }
+    }
+}
+
+/* dit_vk.cpp:295-302: sin half first, then cos half */
+void orc_sinusoidal(float t, int dim, float* e) {
+    int half = dim / 2;
+    for (int j = 0; j < dim; j++) {
+        float freq = (j < half) ? (float)exp(-logf(10000.f) * j / half)
+                                : (float)exp(-logf(10000.f) * (j - half) / half);
+        e[j] = (j < half) ? sinf(t * freq) : cosf(t * freq);
+    }
+}
+
+void orc_silu(float* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) x[i] = x[i] / (1.f + expf(-x[i]));
+}
+
+/* dit_vk.cpp:303-309 */
+void orc_time_embedding(float t, const float* w_in, const float* b_in,
+                        const float* w_hid, const float* b_hid,
+                        const float* w_out, const float* b_out, float* emb) {
+    float e0[256];
+    float* e1 = (float*)malloc(sizeof(float) * DIM);
+    float* e2 = (float*)malloc(sizeof(float) * DIM);
+    orc_sinusoidal(t, 256, e0);
+    orc_linear(e0, w_in, b_in, 1, 256, DIM, e1, 1);
+    orc_silu(e1, DIM);
+    orc_linear(e1, w_hid, b_hid, 1, DIM, DIM, e2, 1);
+    orc_silu(e2, DIM);
+    orc_linear(e2, w_out, b_out, 1, DIM, ORC_EMB, emb, 1);
+    free(e1); free(e2);
+}
+
+/* swiglu (dit_vk.cpp:465-472): out( silu(gate(x)) * in(x) ), no biases */
+static void swiglu(const orc_branch* B, const float* x, int Ln, int mlp, float* y,
+                   int nthreads) {
+    size_t n = (size_t)Ln * mlp;
+    float* h = (float*)malloc(sizeof(float) * n);
+    float* g = (float*)malloc(sizeof(float) * n);
+    orc_linear(x, B->mlp_in_w, NULL, Ln, DIM, mlp, h, nthreads);
+    orc_linear(x, B->mlp_g_w, NULL, Ln, DIM, mlp, g, nthreads);
+    for (size_t k = 0; k < n; k++) g[k] = (g[k] / (1.f + expf(-g[k]))) * h[k];
+    orc_linear(g, B->mlp_out_w, NULL, Ln, mlp, DIM, y, nthreads);
+    free(h); free(g);
+}
+
+/* One layer of DitVk::forward_latent (dit_vk.cpp:517-632) */
+void orc_dit_layer(float* vid, float* txt, int Lv, int TXT, const float* emb,
+                   const orc_branch* vR, const orc_branch* tR, int mlp,
+                   int T, int H, int W, const int32_t* slices, int nwin,
+                   const float* vid_freq, const float* txt_freq, float eps,
+                   int last, int nthreads) {
+    size_t nv = (size_t)Lv * DIM, nt = (size_t)TXT * DIM;
+    float* vid_an = (float*)malloc(sizeof(float) * nv);
+    float* txt_an = (float*)malloc(sizeof(float) * (nt ? nt : 1));
+    for (int t = 0; t < Lv; t++) orc_rmsnorm(vid + (size_t)t * DIM, DIM, NULL, eps, vid_an + (size_t)t * DIM);
+    for (int t = 0; t < TXT; t++) orc_rmsnorm(txt + (size_t)t * DIM, DIM, NULL, eps, txt_an + (size_t)t * DIM);
+    for (int t = 0; t < Lv; t++)
+        for (int d = 0; d < DIM; d++) {
+            float sA = emb[d * 6], scA = emb[d * 6 + 1];
+            float shB = vR->attn_shift[d], scB = vR->attn_scale[d];
+            vid_an[(size_t)t * DIM + d] = vid_an[(size_t)t * DIM + d] * (scA + scB) + (sA + shB);
+        }
+    if (!last)
+        for (int t = 0; t < TXT; t++)
+            for (int d = 0; d < DIM; d++) {
+                float sA = emb[d * 6], scA = emb[d * 6 + 1];
+                float thB = tR->attn_shift[d], tcB = tR->attn_scale[d];
+                txt_an[(size_t)t * DIM + d] = txt_an[(size_t)t * DIM + d] * (scA + tcB) + (sA + thB);
+            }
+    /* DitVk::awa_forward (dit_vk.cpp:312-463): qkv projections, AWA, out */
+    float* vqkv = (float*)malloc(sizeof(float) * (size_t)Lv * QKV);
+    float* tqkv = (float*)malloc(sizeof(float) * (size_t)(TXT ? TXT : 1) * QKV);
+    orc_linear(vid_an, vR->qkv_w, NULL, Lv, DIM, QKV, vqkv, nthreads);
+    orc_linear(txt_an, tR->qkv_w, NULL, TXT, DIM, QKV, tqkv, nthreads);
+    float* vattn = (float*)malloc(sizeof(float) * nv);
+    float* tattn = (float*)malloc(sizeof(float) * (nt ? nt : 1));
+    orc_awa_forward(vqkv, tqkv, Lv, TXT, T, H, W, slices, nwin, vid_freq, txt_freq,
+                    vR->nq, vR->nk, tR->nq, tR->nk, eps, vattn, tattn, nthreads);
+    float* vid_at = (float*)malloc(sizeof(float) * nv);
+    float* txt_at = (float*)malloc(sizeof(float) * (nt ? nt : 1));
+    orc_linear(vattn, vR->out_w, vR->out_b, Lv, DIM, DIM, vid_at, nthreads);
+    orc_linear(tattn, tR->out_w, tR->out_b, TXT, DIM, DIM, txt_at, nthreads);
+    free(vqkv); free(tqkv); free(vattn); free(tattn);
+    /* gate + residual (dit_vk.cpp:558-575) */
+    for (int t = 0; t < Lv; t++)
+        for (int d = 0; d < DIM; d++) {
+            float gA = emb[d * 6 + 2], gB = vR->attn_gate[d];
+            vid_at[(size_t)t * DIM + d] *= (gA + gB);
+        }
+    if (!last)
+        for (int t = 0; t < TXT; t++)
+            for (int d = 0; d < DIM; d++) {
+                float gA = emb[d * 6 + 2], tgB = tR->attn_gate[d];
+                txt_at[(size_t)t * DIM + d] *= (gA + tgB);
+            }
+    for (size_t k = 0; k < nv; k++) vid[k] = vid_at[k] + vid[k];
+    for (size_t k = 0; k < nt; k++) txt[k] = txt_at[k] + txt[k];
+    /* MLP norm + ada (dit_vk.cpp:577-597) */
+    float* vid_mn = vid_an; /* reuse */
+    float* txt_mn = txt_an;
+    for (int t = 0; t < Lv; t++) orc_rmsnorm(vid + (size_t)t * DIM, DIM, NULL, eps, vid_mn + (size_t)t * DIM);
+    if (!last) {
+        for (int t = 0; t < TXT; t++) orc_rmsnorm(txt + (size_t)t * DIM, DIM, NULL, eps, txt_mn + (size_t)t * DIM);
+    } else {
+        memcpy(txt_mn, txt, sizeof(float) * nt);
+    }
+    for (int t = 0; t < Lv; t++)
+        for (int d = 0; d < DIM; d++) {
+            float sAm = emb[d * 6 + 3], scAm = emb[d * 6 + 4];
+            float shB = vR->mlp_shift[d], scB = vR->mlp_scale[d];
+            vid_mn[(size_t)t * DIM + d] = vid_mn[(size_t)t * DIM + d] * (scAm + scB) + (sAm + shB);
+        }
+    if (!last)
+        for (int t = 0; t < TXT; t++)
+            for (int d = 0; d < DIM; d++) {
+                float sAm = emb[d * 6 + 3], scAm = emb[d * 6 + 4];
+                float thB = tR->mlp_shift[d], tcB = tR->mlp_scale[d];
+                txt_mn[(size_t)t * DIM + d] = txt_mn[(size_t)t * DIM + d] * (scAm + tcB) + (sAm + thB);
+            }
+    /* SwiGLU, gate, residual (dit_vk.cpp:608-632) */
+    swiglu(vR, vid_mn, Lv, mlp, vid_at, nthreads);
+    if (!last) swiglu(tR, txt_mn, TXT, mlp, txt_at, nthreads);
+    else memset(txt_at, 0, sizeof(float) * nt);
+    for (int t = 0; t < Lv; t++)
+        for (int d = 0; d < DIM; d++) {
+            float gAm = emb[d * 6 + 5], gB = vR->mlp_gate[d];
+            vid_at[(size_t)t * DIM + d] *= (gAm + gB);
+        }
+    if (!last)
+        for (int t = 0; t < TXT; t++)
+            for (int d = 0; d < DIM; d++) {
+                float gAm = emb[d * 6 + 5], gB = tR->mlp_gate[d];
+                txt_at[(size_t)t * DIM + d] *= (gAm + gB);
+            }
+    for (size_t k = 0; k < nv; k++) vid[k] = vid_at[k] + vid[k];
+    for (size_t k = 0; k < nt; k++) txt[k] = txt_at[k] + txt[k];
+    free(vid_an); free(txt_an); free(vid_at); free(txt_at);
+}

@@ -1,0 +1,108 @@
+// ref_bridge.cpp — exposes the reference's own CPU routines (TEST INFRASTRUCTURE).
+//
+// Compiles the reference's src/verify_dit.cpp unchanged (it needs only the C++
+// standard library and OpenMP) and exports C entry points over its static
+// functions, so tests can compare the oracle with the reference bit for bit.
+// Built by oracle/Makefile into oracle/_ref/ only when the reference sources
+// are present; nothing in the product links it.
+//
+// verify_dit.cpp's main() is renamed so this file can provide the library.
+#define main verify_dit_reference_main
+#include "verify_dit.cpp"
+#undef main
+
+#include <cstdint>
+
+namespace {
+
+LinearRaw make_linear(const float* W, const float* b, int in, int out) {
+    LinearRaw L;
+    L.in = in;
+    L.out = out;
+    L.W.assign(W, W + (size_t)in * out);
+    if (b) L.b.assign(b, b + out);
+    return L;
+}
+
+LinearRaw identity_linear(int n) {
+    LinearRaw L;
+    L.in = n;
+    L.out = n;
+    L.W.assign((size_t)n * n, 0.f);
+    for (int i = 0; i < n; i++) L.W[(size_t)i * n + i] = 1.f;
+    return L;
+}
+
+Win make_ref_win(int t, int h, int w, const int32_t* slices, int nwin,
+                 const float* vid_freq, int sumf, const float* txt_freq, int txt_len) {
+    Win win;
+    win.t = t; win.h = h; win.w = w; win.nwin = nwin;
+    for (int i = 0; i < nwin; i++) {
+        win.st.push_back(slices[i * 6 + 0]); win.en.push_back(slices[i * 6 + 1]);
+        win.sh.push_back(slices[i * 6 + 2]); win.eh.push_back(slices[i * 6 + 3]);
+        win.sw.push_back(slices[i * 6 + 4]); win.ew.push_back(slices[i * 6 + 5]);
+    }
+    win.vid_freq.assign(vid_freq, vid_freq + (size_t)sumf * ROPE_ROT);
+    win.txt_freq.assign(txt_freq, txt_freq + (size_t)nwin * txt_len * ROPE_ROT);
+    return win;
+}
+
+}  // namespace
+
+extern "C" {
+
+void ref_rmsnorm(const float* x, int n, const float* w, float* out) { rmsnorm(x, n, w, out); }
+void ref_qk_norm(const float* x, const float* w, float* out) { qk_norm(x, w, out); }
+void ref_apply_rope(const float* freq, const float* q, float* out) { apply_rope(freq, q, out); }
+void ref_sinusoidal(float t, int dim, float* e) {
+    std::vector<float> v = sinusoidal(t, dim);
+    for (int i = 0; i < dim; i++) e[i] = v[i];
+}
+void ref_silu(float* x, int n) {
+    std::vector<float> v(x, x + n);
+    silu(v);
+    for (int i = 0; i < n; i++) x[i] = v[i];
+}
+void ref_linear(const float* x, const float* W, const float* b, int Ln, int in, int out, float* y) {
+    LinearRaw L = make_linear(W, b, in, out);
+    L.run(x, y, Ln);
+}
+
+// verify_dit.cpp::time_embedding with the given weights (biased linears).
+void ref_time_embedding(float t, const float* w_in, const float* b_in, const float* w_hid,
+                        const float* b_hid, const float* w_out, const float* b_out, float* emb) {
+    g_emb_in = make_linear(w_in, b_in, 256, DIM);
+    g_emb_hid = make_linear(w_hid, b_hid, DIM, DIM);
+    g_emb_out = make_linear(w_out, b_out, DIM, 6 * DIM);
+    std::vector<float> e = time_embedding(t);
+    for (size_t i = 0; i < e.size(); i++) emb[i] = e[i];
+}
+
+// verify_dit.cpp::awa_forward with the given qkv projections and an identity
+// out-projection (no bias), so vid_out/txt_out are the raw attention outputs.
+// Also returns the projected vqkv/tqkv it used (computed by LinearRaw::run).
+// Requires TXT_LEN-independent geometry: freqs are passed in.
+void ref_awa_block(const float* vid, int Lv, const float* txt, int TXT, int t, int h, int w,
+                   const int32_t* slices, int nwin, const float* vid_freq, int sumf,
+                   const float* txt_freq, const float* wqkv_v, const float* wqkv_t,
+                   const float* nq_v, const float* nk_v, const float* nq_t, const float* nk_t,
+                   float* vqkv_out, float* tqkv_out, float* vattn, float* tattn) {
+    static BranchW vW, tW;
+    vW.qkv = make_linear(wqkv_v, nullptr, DIM, QKV);
+    tW.qkv = make_linear(wqkv_t, nullptr, DIM, QKV);
+    if (vW.out.in != DIM) vW.out = identity_linear(DIM);
+    if (tW.out.in != DIM) tW.out = identity_linear(DIM);
+    vW.nq.assign(nq_v, nq_v + HEAD_D); vW.nk.assign(nk_v, nk_v + HEAD_D);
+    tW.nq.assign(nq_t, nq_t + HEAD_D); tW.nk.assign(nk_t, nk_t + HEAD_D);
+    Win win = make_ref_win(t, h, w, slices, nwin, vid_freq, sumf, txt_freq, TXT);
+    std::vector<float> v(vid, vid + (size_t)Lv * DIM), tx(txt, txt + (size_t)TXT * DIM);
+    std::vector<float> vq = vW.qkv.batch(v, Lv), tq = tW.qkv.batch(tx, TXT);
+    for (size_t i = 0; i < vq.size(); i++) vqkv_out[i] = vq[i];
+    for (size_t i = 0; i < tq.size(); i++) tqkv_out[i] = tq[i];
+    std::vector<float> vo, to;
+    awa_forward(v, tx, win, vW, tW, vo, to);
+    for (size_t i = 0; i < vo.size(); i++) vattn[i] = vo[i];
+    for (size_t i = 0; i < to.size(); i++) tattn[i] = to[i];
+}
+
+}  // extern "C"

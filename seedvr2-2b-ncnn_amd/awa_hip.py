@@ -1,0 +1,235 @@
+"""Python binding of the C ABI in include/awa_capi.h (ctypes over lib/libseedvr2_awa.so).
+
+This is the binding a Python caller (and the test-suite and bench) uses; the
+product is the C ABI itself.  Device buffers are torch tensors on a ROCm
+device; the stream is torch's current stream.  There is no fallback: if the
+shared library is missing, import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libseedvr2_awa.so")
+HEADER_DIR = os.path.join(os.path.dirname(HERE), "include")
+
+AWA_OK, AWA_EARG, AWA_EHIP = 0, -1, -2
+AWA_F32, AWA_BF16 = 0, 1
+HEADS, HEAD_D, DIM, QKV, ROPE_ROT = 20, 128, 2560, 7680, 126
+
+_lib = None
+
+
+class AwaError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"AWA error {code}: {msg}")
+        self.code = code
+
+
+class GeomInfo(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in
+                ("t", "h", "w", "nwin", "sumf", "Lv", "txt_len", "max_S", "n_tiles", "n_items")]
+
+
+def build():
+    """Compile lib/libseedvr2_awa.so with hipcc for gfx950."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE, f"-j{min(8, os.cpu_count() or 1)}"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it (make -C {HERE}) before use")
+        L = C.CDLL(LIB_PATH)
+        vp, i32p, f32p = C.c_void_p, C.POINTER(C.c_int32), C.POINTER(C.c_float)
+        L.awa_create.argtypes = [C.POINTER(vp), C.c_int]
+        L.awa_destroy.argtypes = [vp]
+        L.awa_destroy.restype = None
+        L.awa_last_error.argtypes = [vp]
+        L.awa_last_error.restype = C.c_char_p
+        L.awa_plan_windows.argtypes = [C.c_int, C.c_int, C.c_int, i32p, C.c_int, i32p, C.c_int]
+        L.awa_geom_build.argtypes = [vp, C.c_int, C.c_int, C.c_int, i32p, C.c_int, C.c_int,
+                                     C.POINTER(vp), vp]
+        L.awa_geom_set.argtypes = [vp, f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int,
+                                   C.POINTER(vp), vp]
+        L.awa_geom_query.argtypes = [vp, C.POINTER(GeomInfo)]
+        L.awa_geom_read.argtypes = [vp, vp, vp, vp, vp, vp, vp]
+        L.awa_geom_destroy.argtypes = [vp]
+        L.awa_geom_destroy.restype = None
+        L.awa_forward.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
+                                  C.c_float, vp, vp, vp]
+        L.awa_forward_host.argtypes = [vp, vp, f32p, f32p, C.c_int, C.c_int, f32p, f32p, f32p, f32p,
+                                       C.c_float, f32p, f32p]
+        L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
+        L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
+        _lib = L
+    return _lib
+
+
+def header_symbols():
+    """Function names declared in include/*.h."""
+    import re
+    names = []
+    for fn in sorted(os.listdir(HEADER_DIR)):
+        if fn.endswith(".h"):
+            txt = open(os.path.join(HEADER_DIR, fn)).read()
+            txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+            names += re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s+\**([a-z_][a-z0-9_]*)\s*\(",
+                                txt, flags=re.M)
+    return names
+
+
+def _ptr(a):
+    return C.cast(a.ctypes.data, C.POINTER(C.c_int32)) if a is not None else None
+
+
+def plan_windows(t, h, w, num_windows, shifted):
+    """Host-only window planner (awa_plan_windows): returns int32 [nwin, 6]."""
+    nw = np.ascontiguousarray(num_windows, np.int32)
+    n = lib().awa_plan_windows(t, h, w, _ptr(nw), int(bool(shifted)), None, 0)
+    if n < 0:
+        raise AwaError(n, "awa_plan_windows rejected the sizes")
+    out = np.zeros((max(n, 1), 6), np.int32)
+    lib().awa_plan_windows(t, h, w, _ptr(nw), int(bool(shifted)), _ptr(out), n)
+    return out[:n]
+
+
+def _stream_ptr(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class Context:
+    """awa_ctx: one per device and stream (owns the op's scratch)."""
+
+    def __init__(self, device=0):
+        self.ptr = C.c_void_p()
+        rc = lib().awa_create(C.byref(self.ptr), int(device))
+        if rc != AWA_OK:
+            raise AwaError(rc, f"awa_create(device={device}) failed")
+        self.device = int(device)
+
+    def error(self):
+        return lib().awa_last_error(self.ptr).decode()
+
+    def check(self, rc, what):
+        if rc != AWA_OK:
+            raise AwaError(rc, f"{what}: {self.error()}")
+
+    def close(self):
+        if self.ptr:
+            lib().awa_destroy(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- geometry
+    def build_geometry(self, t, h, w, num_windows, txt_len, shifted, stream=None):
+        g = C.c_void_p()
+        nw = np.ascontiguousarray(num_windows, np.int32)
+        rc = lib().awa_geom_build(self.ptr, t, h, w, _ptr(nw), txt_len, int(bool(shifted)),
+                                  C.byref(g), _stream_ptr(stream))
+        self.check(rc, "awa_geom_build")
+        return Geometry(self, g)
+
+    def set_geometry(self, vidx, cumf, vfreq, tfreq, nwin, Lv, txt_len, stream=None):
+        """AwaLayer::set_window_geometry with the reference's float-encoded arrays."""
+        arrs = [np.ascontiguousarray(a, np.float32) for a in (vidx, cumf, vfreq, tfreq)]
+        fp = [a.ctypes.data_as(C.POINTER(C.c_float)) for a in arrs]
+        g = C.c_void_p()
+        rc = lib().awa_geom_set(self.ptr, *fp, int(nwin), int(Lv), int(txt_len), C.byref(g),
+                                _stream_ptr(stream))
+        self.check(rc, "awa_geom_set")
+        return Geometry(self, g)
+
+    # ---- the op
+    def forward(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, eps=1e-5, vattn=None, tattn=None,
+                stream=None):
+        """AwaLayer::forward: torch tensors on the device; returns (vattn, tattn)."""
+        import torch
+        if vqkv.dtype == torch.bfloat16:
+            dtype = AWA_BF16
+        elif vqkv.dtype == torch.float32:
+            dtype = AWA_F32
+        else:
+            raise TypeError(f"unsupported dtype {vqkv.dtype}")
+        if tqkv.dtype != vqkv.dtype:
+            raise TypeError("vqkv and tqkv must share a dtype")
+        for t_ in (vqkv, tqkv):
+            if not t_.is_cuda or not t_.is_contiguous():
+                raise ValueError("inputs must be contiguous device tensors")
+        Lv, TXT = vqkv.shape[0], tqkv.shape[0]
+        if vqkv.shape[1] != QKV or tqkv.shape[1] != QKV:
+            raise ValueError("rows must have 7680 columns (q|k|v)")
+        gains = [g.to(device=vqkv.device, dtype=torch.float32).contiguous() for g in (nq_v, nk_v, nq_t, nk_t)]
+        if vattn is None:
+            vattn = torch.empty((Lv, DIM), dtype=vqkv.dtype, device=vqkv.device)
+        if tattn is None:
+            tattn = torch.empty((TXT, DIM), dtype=vqkv.dtype, device=vqkv.device)
+        rc = lib().awa_forward(self.ptr, geom.ptr, dtype, C.c_void_p(vqkv.data_ptr()),
+                               C.c_void_p(tqkv.data_ptr()), Lv, TXT,
+                               *[C.c_void_p(g.data_ptr()) for g in gains], float(eps),
+                               C.c_void_p(vattn.data_ptr()), C.c_void_p(tattn.data_ptr()),
+                               _stream_ptr(stream))
+        self.check(rc, "awa_forward")
+        self._keep = gains  # alive until the stream consumed them
+        return vattn, tattn
+
+    def forward_host(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, eps=1e-5):
+        """AwaVk::forward: numpy fp32 in and out, synchronous."""
+        f = lambda a: np.ascontiguousarray(a, np.float32)
+        vqkv, tqkv = f(vqkv), f(tqkv)
+        g4 = [f(x) for x in (nq_v, nk_v, nq_t, nk_t)]
+        Lv, TXT = vqkv.shape[0], tqkv.shape[0]
+        vo = np.empty((Lv, DIM), np.float32)
+        to = np.empty((TXT, DIM), np.float32)
+        P = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+        rc = lib().awa_forward_host(self.ptr, geom.ptr, P(vqkv), P(tqkv), Lv, TXT, *[P(x) for x in g4],
+                                    float(eps), P(vo), P(to))
+        self.check(rc, "awa_forward_host")
+        return vo, to
+
+
+class Geometry:
+    def __init__(self, ctx, ptr):
+        self.ctx = ctx
+        self.ptr = ptr
+
+    def info(self):
+        gi = GeomInfo()
+        rc = lib().awa_geom_query(self.ptr, C.byref(gi))
+        if rc != AWA_OK:
+            raise AwaError(rc, "awa_geom_query")
+        return {n: getattr(gi, n) for n, _ in GeomInfo._fields_}
+
+    def read(self):
+        i = self.info()
+        sl = np.zeros((i["nwin"], 6), np.int32)
+        cumf = np.zeros(i["nwin"] + 1, np.int32)
+        vidx = np.zeros(i["sumf"], np.int32)
+        vf = np.zeros((i["sumf"], ROPE_ROT), np.float32)
+        tf = np.zeros((i["nwin"] * i["txt_len"], ROPE_ROT), np.float32)
+        rc = lib().awa_geom_read(self.ctx.ptr, self.ptr, *[C.c_void_p(a.ctypes.data) for a in (sl, cumf, vidx, vf, tf)])
+        self.ctx.check(rc, "awa_geom_read")
+        return {"slices": sl, "cumf": cumf, "vidx": vidx, "vid_freq": vf, "txt_freq": tf}
+
+    def close(self):
+        if self.ptr:
+            lib().awa_geom_destroy(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,593 @@
+// awa_capi.cpp — C ABI of the AWA op: contexts, geometry, forward.
+//
+// Host C++17.  Computes the geometry plan (window sizes, 64-row tiles, work
+// items) with the same integer formulas the device kernel uses, owns the
+// device buffers, and enqueues pack -> SDPA -> coalesce on the caller's
+// stream without synchronising.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "awa_internal.hpp"
+
+using namespace awa;
+
+namespace {
+
+void set_err(awa_ctx* ctx, const char* fmt, ...) {
+    if (!ctx) return;
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    ctx->err = buf;
+}
+
+// Makes ctx->device current for the scope and restores the caller's device.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        ok = (prev == dev) || (hipSetDevice(dev) == hipSuccess);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+#define HIPCK(ctx, expr)                                                                     \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) {                                                              \
+            set_err(ctx, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,    \
+                    __LINE__);                                                               \
+            return AWA_EHIP;                                                                 \
+        }                                                                                    \
+    } while (0)
+
+template <typename T>
+hipError_t dalloc(T** p, size_t n) {
+    *p = nullptr;
+    if (n == 0) n = 1;
+    return hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T));
+}
+
+void free_geom_buffers(awa_geom* g) {
+    void* ptrs[] = {g->d_slices, g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win,
+                    g->d_items, g->d_vfreq, g->d_tfreq, g->d_vcs, g->d_tcs};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+}
+
+// 64-row tiles of every window plus the text tiles, and the work items of the
+// attention kernel (one window, two query tiles).
+void plan_tiles(GeomPlan& P) {
+    P.ntt = (P.txt_len + TILE - 1) / TILE;
+    P.tile_base.assign(P.nwin + 1, 0);
+    P.tile_win.clear();
+    P.max_S = 0;
+    for (int w = 0; w < P.nwin; w++) {
+        const int f = P.cumf[w + 1] - P.cumf[w];
+        const int nvt = (f + TILE - 1) / TILE;
+        P.tile_base[w + 1] = P.tile_base[w] + nvt;
+        for (int k = 0; k < nvt; k++) P.tile_win.push_back(w);
+        if (f + P.txt_len > P.max_S) P.max_S = f + P.txt_len;
+    }
+    P.n_vid_tiles = P.tile_base[P.nwin];
+    P.n_tiles = P.n_vid_tiles + P.txt_sets * P.ntt;
+    P.items.clear();
+    for (int w = 0; w < P.nwin; w++) {
+        const int nq = (P.tile_base[w + 1] - P.tile_base[w]) + P.ntt;
+        for (int q = 0; q < nq; q += 2) {
+            P.items.push_back(w);
+            P.items.push_back(q);
+            P.items.push_back(q + 1 < nq ? q + 1 : -1);
+            P.items.push_back(0);
+        }
+    }
+    P.n_items = (int)P.items.size() / 4;
+}
+
+int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
+    const GeomPlan& P = g->plan;
+    HIPCK(ctx, dalloc(&g->d_tile_base, P.tile_base.size()));
+    HIPCK(ctx, dalloc(&g->d_tile_win, P.tile_win.size()));
+    HIPCK(ctx, dalloc(&g->d_items, P.items.size()));
+    HIPCK(ctx, hipMemcpyAsync(g->d_tile_base, P.tile_base.data(), P.tile_base.size() * 4,
+                              hipMemcpyHostToDevice, s));
+    if (!P.tile_win.empty())
+        HIPCK(ctx, hipMemcpyAsync(g->d_tile_win, P.tile_win.data(), P.tile_win.size() * 4,
+                                  hipMemcpyHostToDevice, s));
+    if (!P.items.empty())
+        HIPCK(ctx, hipMemcpyAsync(g->d_items, P.items.data(), P.items.size() * 4,
+                                  hipMemcpyHostToDevice, s));
+    return AWA_OK;
+}
+
+
+// Window sizes (awa_window.cpp:21-26, in double as the reference) and the
+// non-empty slices of each axis with the integer formulas of Axis.
+struct AxisSlices {
+    int cnt[3];
+    std::vector<int> st[3], en[3];
+};
+
+int plan_axes(int t, int h, int w, const int32_t num_windows[3], int shifted, GeomParams& p,
+              AxisSlices& out, awa_ctx* ctx) {
+    if (t < 1 || h < 1 || w < 1 || num_windows[0] < 1 || num_windows[1] < 1 || num_windows[2] < 1) {
+        set_err(ctx, "window plan: bad sizes t=%d h=%d w=%d nw=(%d,%d,%d)", t, h, w, num_windows[0],
+                num_windows[1], num_windows[2]);
+        return AWA_EARG;
+    }
+    if ((long)t * h * w > (1L << 24)) {
+        set_err(ctx, "window plan: grid too large");
+        return AWA_EARG;
+    }
+    const double scale = std::sqrt((45.0 * 80.0) / ((double)h * w));
+    const int resized_h = (int)std::round(h * scale);
+    const int resized_w = (int)std::round(w * scale);
+    const int wh = (resized_h + num_windows[1] - 1) / num_windows[1];
+    const int ww = (resized_w + num_windows[2] - 1) / num_windows[2];
+    const int wt = ((t < 30 ? t : 30) + num_windows[0] - 1) / num_windows[0];
+    const int ext[3] = {t, h, w}, win[3] = {wt, wh, ww};
+    for (int a = 0; a < 3; a++) {
+        if (win[a] < 1) {
+            set_err(ctx, "window plan: empty window size on axis %d", a);
+            return AWA_EARG;
+        }
+        p.ax[a].X = ext[a];
+        p.ax[a].wX = win[a];
+        p.ax[a].shifted_variant = shifted ? 1 : 0;
+        p.ax[a].shift = (shifted && win[a] < ext[a]) ? 1 : 0;
+        const int n = p.ax[a].count();
+        out.st[a].clear();
+        out.en[a].clear();
+        for (int i = 0; i < n; i++) {
+            int s0, e0;
+            p.ax[a].slice(i, &s0, &e0);
+            if (e0 > s0) {
+                out.st[a].push_back(s0);
+                out.en[a].push_back(e0);
+            }
+        }
+        out.cnt[a] = (int)out.st[a].size();
+        if (out.cnt[a] < 1 || out.cnt[a] > MAX_AXIS) {
+            set_err(ctx, "window plan: %d windows on axis %d (limit %d)", out.cnt[a], a, MAX_AXIS);
+            return AWA_EARG;
+        }
+    }
+    const long nwin = (long)out.cnt[0] * out.cnt[1] * out.cnt[2];
+    if (nwin > MAX_WIN) {
+        set_err(ctx, "window plan: %ld windows (limit %d)", nwin, MAX_WIN);
+        return AWA_EARG;
+    }
+    return AWA_OK;
+}
+
+size_t elem_size(int dtype) { return dtype == AWA_BF16 ? 2 : 4; }
+
+int ensure_scratch(awa_ctx* ctx, size_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return AWA_OK;
+    if (ctx->scratch) {
+        // hipFree waits for work still using the old buffer.
+        HIPCK(ctx, hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+    }
+    HIPCK(ctx, hipMalloc(&ctx->scratch, bytes));
+    ctx->scratch_bytes = bytes;
+    return AWA_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+int awa_create(awa_ctx** out, int hip_device) {
+    if (!out) return AWA_EARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || hip_device < 0 || hip_device >= n) return AWA_EHIP;
+    awa_ctx* ctx = new (std::nothrow) awa_ctx();
+    if (!ctx) return AWA_EHIP;
+    ctx->device = hip_device;
+    *out = ctx;
+    return AWA_OK;
+}
+
+void awa_destroy(awa_ctx* ctx) {
+    if (!ctx) return;
+    DeviceGuard dg(ctx->device);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    delete ctx;
+}
+
+const char* awa_last_error(const awa_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int awa_plan_windows(int t, int h, int w, const int32_t num_windows[3], int shifted,
+                     int32_t* h_slices, int cap) {
+    if (!num_windows || cap < 0 || (cap > 0 && !h_slices)) return AWA_EARG;
+    GeomParams p{};
+    AxisSlices ax;
+    if (plan_axes(t, h, w, num_windows, shifted, p, ax, nullptr) != AWA_OK) return AWA_EARG;
+    const int nwin = ax.cnt[0] * ax.cnt[1] * ax.cnt[2];
+    for (int wi = 0; wi < nwin && wi < cap; wi++) {
+        const int it = wi % ax.cnt[0], ih = (wi / ax.cnt[0]) % ax.cnt[1];
+        const int iw = wi / (ax.cnt[0] * ax.cnt[1]);
+        int32_t* sl = h_slices + (size_t)wi * 6;
+        sl[0] = ax.st[0][it]; sl[1] = ax.en[0][it];
+        sl[2] = ax.st[1][ih]; sl[3] = ax.en[1][ih];
+        sl[4] = ax.st[2][iw]; sl[5] = ax.en[2][iw];
+    }
+    return nwin;
+}
+
+int awa_geom_build(awa_ctx* ctx, int t, int h, int w, const int32_t num_windows[3], int txt_len,
+                   int shifted, awa_geom** out, awa_stream_t stream) {
+    if (!ctx || !out || !num_windows) {
+        set_err(ctx, "awa_geom_build: null argument");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    if (t < 1 || h < 1 || w < 1 || txt_len < 1 || num_windows[0] < 1 || num_windows[1] < 1 ||
+        num_windows[2] < 1) {
+        set_err(ctx, "awa_geom_build: bad sizes t=%d h=%d w=%d txt=%d nw=(%d,%d,%d)", t, h, w,
+                txt_len, num_windows[0], num_windows[1], num_windows[2]);
+        return AWA_EARG;
+    }
+    if ((long)t * h * w > (1L << 24)) {
+        set_err(ctx, "awa_geom_build: grid too large");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+    GeomParams p{};
+    AxisSlices ax;
+    int rc0 = plan_axes(t, h, w, num_windows, shifted, p, ax, ctx);
+    if (rc0 != AWA_OK) return rc0;
+    const int* cnt = ax.cnt;
+    const std::vector<int>* st = ax.st;
+    const std::vector<int>* en = ax.en;
+    const long nwin = (long)cnt[0] * cnt[1] * cnt[2];
+    awa_geom* g = new (std::nothrow) awa_geom();
+    if (!g) return AWA_EHIP;
+    g->device = ctx->device;
+    GeomPlan& P = g->plan;
+    P.t = t; P.h = h; P.w = w; P.txt_len = txt_len; P.nwin = (int)nwin; P.Lv = t * h * w;
+    P.txt_sets = 1;
+    P.cumf.assign(P.nwin + 1, 0);
+    for (int wi = 0; wi < P.nwin; wi++) {
+        const int it = wi % cnt[0], ih = (wi / cnt[0]) % cnt[1], iw = wi / (cnt[0] * cnt[1]);
+        const int sl[6] = {st[0][it], en[0][it], st[1][ih], en[1][ih], st[2][iw], en[2][iw]};
+        P.slices.insert(P.slices.end(), sl, sl + 6);
+        P.cumf[wi + 1] = P.cumf[wi] + (sl[1] - sl[0]) * (sl[3] - sl[2]) * (sl[5] - sl[4]);
+    }
+    P.sumf = P.cumf[P.nwin];
+    P.covers_all = (P.sumf == P.Lv);  // windows tile the grid (every token once)
+    plan_tiles(P);
+
+    p.t = t; p.h = h; p.w = w; p.txt_len = txt_len; p.nwin = P.nwin; p.sumf = P.sumf;
+    for (int j = 0; j < 21; j++) p.base[j] = 1.0 / std::pow(10000.0, (double)(j * 2) / 42);
+
+    int rc = AWA_OK;
+    auto fail = [&](hipError_t e, const char* what) {
+        set_err(ctx, "awa_geom_build: %s: %s", what, hipGetErrorString(e));
+        rc = AWA_EHIP;
+    };
+    hipError_t e;
+    if ((e = dalloc(&g->d_slices, (size_t)P.nwin * 6)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_cumf, (size_t)P.nwin + 1)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_vidx, (size_t)P.sumf)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_vfreq, (size_t)P.sumf * ROPE_ROT)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_tfreq, (size_t)P.nwin * txt_len * ROPE_ROT)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_vcs, (size_t)P.sumf * NPAIR)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_tcs, (size_t)txt_len * NPAIR)) != hipSuccess) fail(e, "alloc");
+    else if ((e = launch_geom_build(p, g, s)) != hipSuccess) fail(e, "geometry kernel");
+    if (rc == AWA_OK) rc = upload_plan(ctx, g, s);
+    if (rc == AWA_OK) {
+        // The plan vectors are pageable; make sure the copies have consumed
+        // them before the caller can touch the geometry.
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) fail(e, "sync");
+    }
+    if (rc != AWA_OK) {
+        free_geom_buffers(g);
+        delete g;
+        return rc;
+    }
+    *out = g;
+    return AWA_OK;
+}
+
+int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf, const float* h_vfreq,
+                 const float* h_tfreq, int nwin, int Lv, int txt_len, awa_geom** out,
+                 awa_stream_t stream) {
+    if (!ctx || !out || !h_cumf || !h_vfreq || !h_tfreq || !h_vidx) {
+        set_err(ctx, "awa_geom_set: null argument");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    if (nwin < 1 || nwin > MAX_WIN || Lv < 1 || txt_len < 1) {
+        set_err(ctx, "awa_geom_set: bad sizes nwin=%d Lv=%d txt=%d", nwin, Lv, txt_len);
+        return AWA_EARG;
+    }
+    // Decode the float encoding (int(x + 0.5), awa.comp:88,101) and validate.
+    std::vector<int32_t> cumf(nwin + 1);
+    for (int i = 0; i <= nwin; i++) cumf[i] = (int32_t)(h_cumf[i] + 0.5f);
+    if (cumf[0] != 0) {
+        set_err(ctx, "awa_geom_set: cumf[0] = %d, expected 0", cumf[0]);
+        return AWA_EARG;
+    }
+    for (int i = 0; i < nwin; i++)
+        if (cumf[i + 1] < cumf[i]) {
+            set_err(ctx, "awa_geom_set: cumf decreases at window %d", i);
+            return AWA_EARG;
+        }
+    const int sumf = cumf[nwin];
+    if (sumf < 1 || sumf > Lv) {
+        set_err(ctx, "awa_geom_set: sumf=%d outside [1, Lv=%d]", sumf, Lv);
+        return AWA_EARG;
+    }
+    std::vector<int32_t> vidx(sumf);
+    std::vector<uint8_t> seen(Lv, 0);
+    for (int g = 0; g < sumf; g++) {
+        const float x = h_vidx[g];
+        if (!(x > -0.5f) || !(x < (float)Lv - 0.5f)) {
+            set_err(ctx, "awa_geom_set: vidx[%d] = %g outside [0, %d)", g, x, Lv);
+            return AWA_EARG;
+        }
+        const int v = (int)(x + 0.5f);
+        if (seen[v]) {
+            set_err(ctx, "awa_geom_set: token %d appears in two windows", v);
+            return AWA_EARG;
+        }
+        seen[v] = 1;
+        vidx[g] = v;
+    }
+    for (size_t r = 0; r < (size_t)sumf; r++)
+        for (int q = 0; q < NPAIR; q++)
+            if (h_vfreq[r * ROPE_ROT + 2 * q] != h_vfreq[r * ROPE_ROT + 2 * q + 1]) {
+                set_err(ctx, "awa_geom_set: vfreq row %zu channel pair %d differs", r, q);
+                return AWA_EARG;
+            }
+    const size_t trows = (size_t)nwin * txt_len;
+    for (size_t r = 0; r < trows; r++)
+        for (int q = 0; q < NPAIR; q++)
+            if (h_tfreq[r * ROPE_ROT + 2 * q] != h_tfreq[r * ROPE_ROT + 2 * q + 1]) {
+                set_err(ctx, "awa_geom_set: tfreq row %zu channel pair %d differs", r, q);
+                return AWA_EARG;
+            }
+    // Text rows shared by all windows?  (make_win repeats one table, so yes.)
+    bool shared = true;
+    for (int w = 1; w < nwin && shared; w++)
+        shared = std::memcmp(h_tfreq, h_tfreq + (size_t)w * txt_len * ROPE_ROT,
+                             sizeof(float) * txt_len * ROPE_ROT) == 0;
+
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    awa_geom* g = new (std::nothrow) awa_geom();
+    if (!g) return AWA_EHIP;
+    g->device = ctx->device;
+    g->injected = true;
+    GeomPlan& P = g->plan;
+    P.nwin = nwin; P.Lv = Lv; P.txt_len = txt_len; P.sumf = sumf; P.cumf = cumf;
+    P.slices.assign((size_t)nwin * 6, 0);
+    P.txt_sets = shared ? 1 : nwin;
+    P.covers_all = (sumf == Lv);
+    plan_tiles(P);
+    const size_t tcs_rows = (size_t)P.txt_sets * txt_len;
+
+    int rc = AWA_OK;
+    hipError_t e = hipSuccess;
+    auto step = [&](hipError_t x) {
+        if (rc == AWA_OK && x != hipSuccess) {
+            e = x;
+            rc = AWA_EHIP;
+        }
+    };
+    step(dalloc(&g->d_slices, (size_t)nwin * 6));
+    step(dalloc(&g->d_cumf, (size_t)nwin + 1));
+    step(dalloc(&g->d_vidx, (size_t)sumf));
+    step(dalloc(&g->d_vfreq, (size_t)sumf * ROPE_ROT));
+    step(dalloc(&g->d_tfreq, trows * ROPE_ROT));
+    step(dalloc(&g->d_vcs, (size_t)sumf * NPAIR));
+    step(dalloc(&g->d_tcs, tcs_rows * NPAIR));
+    if (rc == AWA_OK) {
+        step(hipMemcpyAsync(g->d_slices, P.slices.data(), P.slices.size() * 4, hipMemcpyHostToDevice, s));
+        step(hipMemcpyAsync(g->d_cumf, cumf.data(), cumf.size() * 4, hipMemcpyHostToDevice, s));
+        step(hipMemcpyAsync(g->d_vidx, vidx.data(), vidx.size() * 4, hipMemcpyHostToDevice, s));
+        step(hipMemcpyAsync(g->d_vfreq, h_vfreq, (size_t)sumf * ROPE_ROT * 4, hipMemcpyHostToDevice, s));
+        step(hipMemcpyAsync(g->d_tfreq, h_tfreq, trows * ROPE_ROT * 4, hipMemcpyHostToDevice, s));
+        step(launch_geom_tables(g->d_vfreq, g->d_tfreq, sumf, (int)tcs_rows, g->d_vcs, g->d_tcs, s));
+    }
+    if (rc == AWA_OK) rc = upload_plan(ctx, g, s);
+    if (rc == AWA_OK) step(hipStreamSynchronize(s));
+    if (rc != AWA_OK) {
+        if (e != hipSuccess) set_err(ctx, "awa_geom_set: %s", hipGetErrorString(e));
+        free_geom_buffers(g);
+        delete g;
+        return rc;
+    }
+    *out = g;
+    return AWA_OK;
+}
+
+int awa_geom_query(const awa_geom* g, awa_geom_info* info) {
+    if (!g || !info) return AWA_EARG;
+    const GeomPlan& P = g->plan;
+    info->t = P.t; info->h = P.h; info->w = P.w;
+    info->nwin = P.nwin; info->sumf = P.sumf; info->Lv = P.Lv; info->txt_len = P.txt_len;
+    info->max_S = P.max_S; info->n_tiles = P.n_tiles; info->n_items = P.n_items;
+    return AWA_OK;
+}
+
+int awa_geom_read(awa_ctx* ctx, const awa_geom* g, int32_t* h_slices, int32_t* h_cumf,
+                  int32_t* h_vidx, float* h_vfreq, float* h_tfreq) {
+    if (!ctx || !g) {
+        set_err(ctx, "awa_geom_read: null argument");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    const GeomPlan& P = g->plan;
+    HIPCK(ctx, hipDeviceSynchronize());
+    if (h_slices) HIPCK(ctx, hipMemcpy(h_slices, g->d_slices, (size_t)P.nwin * 6 * 4, hipMemcpyDeviceToHost));
+    if (h_cumf) HIPCK(ctx, hipMemcpy(h_cumf, g->d_cumf, (size_t)(P.nwin + 1) * 4, hipMemcpyDeviceToHost));
+    if (h_vidx) HIPCK(ctx, hipMemcpy(h_vidx, g->d_vidx, (size_t)P.sumf * 4, hipMemcpyDeviceToHost));
+    if (h_vfreq)
+        HIPCK(ctx, hipMemcpy(h_vfreq, g->d_vfreq, (size_t)P.sumf * ROPE_ROT * 4, hipMemcpyDeviceToHost));
+    if (h_tfreq)
+        HIPCK(ctx, hipMemcpy(h_tfreq, g->d_tfreq, (size_t)P.nwin * P.txt_len * ROPE_ROT * 4,
+                             hipMemcpyDeviceToHost));
+    return AWA_OK;
+}
+
+void awa_geom_destroy(awa_geom* g) {
+    if (!g) return;
+    DeviceGuard dg(g->device);
+    free_geom_buffers(g);
+    delete g;
+}
+
+int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
+                int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
+                const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, awa_stream_t stream) {
+    if (!ctx || !g || !d_vqkv || !d_tqkv || !d_nq_v || !d_nk_v || !d_nq_t || !d_nk_t || !d_vattn ||
+        !d_tattn) {
+        set_err(ctx, "awa_forward: null argument");
+        return AWA_EARG;
+    }
+    const GeomPlan& P = g->plan;
+    if (dtype != AWA_F32 && dtype != AWA_BF16) {
+        set_err(ctx, "awa_forward: unknown dtype %d", dtype);
+        return AWA_EARG;
+    }
+    if (Lv != P.Lv || TXT != P.txt_len) {
+        set_err(ctx, "awa_forward: Lv=%d TXT=%d do not match the geometry (Lv=%d TXT=%d)", Lv, TXT,
+                P.Lv, P.txt_len);
+        return AWA_EARG;
+    }
+    if (!(eps > 0.f)) {
+        set_err(ctx, "awa_forward: eps must be > 0 (got %g)", (double)eps);
+        return AWA_EARG;
+    }
+    if (g->device != ctx->device) {
+        set_err(ctx, "awa_forward: geometry lives on device %d, context on %d", g->device, ctx->device);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const size_t es = elem_size(dtype);
+    const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
+    const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
+    const size_t tpart_bytes = (size_t)P.nwin * P.txt_len * DIM * 4;
+    int rc = ensure_scratch(ctx, off_t + align256(tpart_bytes));
+    if (rc != AWA_OK) return rc;
+    char* base = static_cast<char*>(ctx->scratch);
+
+    if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
+
+    PackArgs pa{};
+    pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
+    pa.nq_v = d_nq_v; pa.nk_v = d_nk_v; pa.nq_t = d_nq_t; pa.nk_t = d_nk_t;
+    pa.cumf = g->d_cumf; pa.vidx = g->d_vidx; pa.tile_base = g->d_tile_base; pa.tile_win = g->d_tile_win;
+    pa.vcs = g->d_vcs; pa.tcs = g->d_tcs;
+    pa.Qp = base; pa.Kp = base + off_k; pa.Vp = base + off_v;
+    pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
+    pa.n_tiles = P.n_tiles; pa.eps = eps;
+    HIPCK(ctx, launch_pack(dtype, pa, s));
+
+    SdpaArgs sa{};
+    sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
+    sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
+    sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
+    sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
+    sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
+    sa.scale_log2e = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
+    HIPCK(ctx, launch_sdpa(dtype, sa, s));
+
+    HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
+    return AWA_OK;
+}
+
+int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv, const float* h_tqkv,
+                     int Lv, int TXT, const float* h_nq_v, const float* h_nk_v, const float* h_nq_t,
+                     const float* h_nk_t, float eps, float* h_vid_out, float* h_txt_out) {
+    if (!ctx || !g || !h_vqkv || !h_tqkv || !h_nq_v || !h_nk_v || !h_nq_t || !h_nk_t ||
+        !h_vid_out || !h_txt_out) {
+        set_err(ctx, "awa_forward_host: null argument");
+        return AWA_EARG;
+    }
+    if (Lv != g->plan.Lv || TXT != g->plan.txt_len) {
+        set_err(ctx, "awa_forward_host: Lv=%d TXT=%d do not match the geometry", Lv, TXT);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    const size_t nv = (size_t)Lv * QKV, nt = (size_t)TXT * QKV;
+    const size_t ov = (size_t)Lv * DIM, ot = (size_t)TXT * DIM;
+    float* buf = nullptr;
+    const size_t total = nv + nt + ov + ot + 4 * HEAD_D;
+    HIPCK(ctx, hipMalloc(reinterpret_cast<void**>(&buf), total * sizeof(float)));
+    float *dv = buf, *dt = dv + nv, *dvo = dt + nt, *dto = dvo + ov, *dg4 = dto + ot;
+    int rc = AWA_OK;
+    auto cp = [&](void* dst, const void* src, size_t bytes, hipMemcpyKind k) {
+        if (rc == AWA_OK) {
+            hipError_t e = hipMemcpy(dst, src, bytes, k);
+            if (e != hipSuccess) {
+                set_err(ctx, "awa_forward_host: copy failed: %s", hipGetErrorString(e));
+                rc = AWA_EHIP;
+            }
+        }
+    };
+    cp(dv, h_vqkv, nv * 4, hipMemcpyHostToDevice);
+    cp(dt, h_tqkv, nt * 4, hipMemcpyHostToDevice);
+    cp(dg4, h_nq_v, HEAD_D * 4, hipMemcpyHostToDevice);
+    cp(dg4 + HEAD_D, h_nk_v, HEAD_D * 4, hipMemcpyHostToDevice);
+    cp(dg4 + 2 * HEAD_D, h_nq_t, HEAD_D * 4, hipMemcpyHostToDevice);
+    cp(dg4 + 3 * HEAD_D, h_nk_t, HEAD_D * 4, hipMemcpyHostToDevice);
+    if (rc == AWA_OK)
+        rc = awa_forward(ctx, g, AWA_F32, dv, dt, Lv, TXT, dg4, dg4 + HEAD_D, dg4 + 2 * HEAD_D,
+                         dg4 + 3 * HEAD_D, eps, dvo, dto, nullptr);
+    if (rc == AWA_OK) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            set_err(ctx, "awa_forward_host: %s", hipGetErrorString(e));
+            rc = AWA_EHIP;
+        }
+    }
+    cp(h_vid_out, dvo, ov * 4, hipMemcpyDeviceToHost);
+    cp(h_txt_out, dto, ot * 4, hipMemcpyDeviceToHost);
+    (void)hipFree(buf);
+    return rc;
+}
+
+int awa_cast_f32_to_bf16(awa_ctx* ctx, const float* d_in, uint16_t* d_out, int64_t n,
+                         awa_stream_t stream) {
+    if (!ctx || (n > 0 && (!d_in || !d_out)) || n < 0) {
+        set_err(ctx, "awa_cast_f32_to_bf16: bad argument");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    HIPCK(ctx, launch_cast_f32_bf16(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));
+    return AWA_OK;
+}
+
+int awa_cast_bf16_to_f32(awa_ctx* ctx, const uint16_t* d_in, float* d_out, int64_t n,
+                         awa_stream_t stream) {
+    if (!ctx || (n > 0 && (!d_in || !d_out)) || n < 0) {
+        set_err(ctx, "awa_cast_bf16_to_f32: bad argument");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    HIPCK(ctx, launch_cast_bf16_f32(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));
+    return AWA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+// awa_coalesce.hip — cross-window text average and boundary casts.
+//
+// tattn[i][c] = (sum over windows w, in window order, of tpart[w][i][c]) / nwin
+// (dit_vk.cpp:440-444, awa_coalesce.comp:19-29): fp32 sums in the same order
+// as the reference, then one division, then the output store (fp32, or bf16
+// rounded to nearest even as cast_f32_bf16.comp:24).  HBM-bound.
+#include "awa_internal.hpp"
+
+namespace awa {
+
+namespace {
+
+__device__ inline uint32_t bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <bool kBf16Out>
+__global__ __launch_bounds__(256) void coalesce_kernel(const float* __restrict__ tpart,
+                                                       void* __restrict__ out, int nwin, int n4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;  // one float4 of [TXT*2560]
+    if (i >= n4) return;
+    const float4* src = reinterpret_cast<const float4*>(tpart) + i;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int w = 0; w < nwin; w++) {
+        const float4 v = src[(size_t)w * n4];
+        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    const float fn = (float)nwin;
+    s.x /= fn; s.y /= fn; s.z /= fn; s.w /= fn;
+    if constexpr (kBf16Out) {
+        uint2 u;
+        u.x = bf16_rne(s.x) | (bf16_rne(s.y) << 16);
+        u.y = bf16_rne(s.z) | (bf16_rne(s.w) << 16);
+        reinterpret_cast<uint2*>(out)[i] = u;
+    } else {
+        reinterpret_cast<float4*>(out)[i] = s;
+    }
+}
+
+__global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* __restrict__ in,
+                                                            uint16_t* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t j = i; j < n; j += stride) out[j] = (uint16_t)bf16_rne(in[j]);
+}
+
+__global__ __launch_bounds__(256) void cast_bf16_f32_kernel(const uint16_t* __restrict__ in,
+                                                            float* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t j = i; j < n; j += stride) out[j] = __uint_as_float((uint32_t)in[j] << 16);
+}
+
+// A fill kernel rather than hipMemsetAsync, so the op stays graph-capturable.
+__global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, size_t n16) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t j = i; j < n16; j += stride) p[j] = make_uint4(0, 0, 0, 0);
+}
+
+inline unsigned grid_for(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    if (b < 1) b = 1;
+    if (b > 65535) b = 65535;
+    return (unsigned)b;
+}
+
+}  // namespace
+
+hipError_t launch_coalesce(int dtype, const float* tpart, void* tattn, int nwin, int txt_len,
+                           hipStream_t s) {
+    const int n4 = txt_len * DIM / 4;
+    const unsigned blocks = (unsigned)((n4 + 255) / 256);
+    if (blocks == 0) return hipSuccess;
+    if (dtype == AWA_BF16)
+        hipLaunchKernelGGL(coalesce_kernel<true>, dim3(blocks), dim3(256), 0, s, tpart, tattn, nwin, n4);
+    else
+        hipLaunchKernelGGL(coalesce_kernel<false>, dim3(blocks), dim3(256), 0, s, tpart, tattn, nwin, n4);
+    return hipGetLastError();
+}
+
+hipError_t launch_cast_f32_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_cast_bf16_f32(const uint16_t* in, float* out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(cast_bf16_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+    const size_t n16 = bytes / 16;  // callers pass multiples of 16 bytes
+    if (n16 == 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_kernel, dim3(grid_for((int64_t)n16)), dim3(256), 0, s,
+                       reinterpret_cast<uint4*>(p), n16);
+    return hipGetLastError();
+}
+
+}  // namespace awa

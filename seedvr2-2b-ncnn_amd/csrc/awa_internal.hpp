@@ -1,0 +1,160 @@
+// awa_internal.hpp — shared definitions of the gfx950 AWA implementation.
+//
+// Packed attention layout (built by the pack kernel, read by the SDPA kernel):
+// every window's video rows are cut into 64-row "tiles"; the text rows form
+// ceil(TXT/64) further tiles, stored once when every window uses the same text
+// RoPE table (always true for make_win geometry) or once per window otherwise.
+// Per head h and tile k the packed buffers hold
+//   Qp[h][k][slot 0..63][d 0..127]   normalised + rotated queries
+//   Kp[h][k][slot 0..63][d 0..127]   normalised + rotated keys
+//   Vp[h][k][d 0..127][slot 0..63]   values, transposed inside the tile
+// in the storage type of the op (bf16 or fp32).  Unused slots are zero.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "awa_capi.h"
+
+namespace awa {
+
+constexpr int HEADS = 20, HEAD_D = 128, DIM = 2560, QKV = 7680;
+constexpr int ROPE_ROT = 126, NPAIR = 63;
+constexpr int TILE = 64;           // rows per packed tile
+constexpr int MAX_AXIS = 256;      // slices per axis accepted by the geometry kernel
+constexpr int MAX_WIN = 4096;      // windows accepted by the geometry kernel
+
+// Integer restatement of awa_window.cpp:15-78 along one axis.  The reference
+// forms shifted bounds as int((i - 0.5) * wX) in double; for integer i and wX
+// that product is an exact half-integer, so C's truncating integer division
+// of (2i - 1) * wX by 2 is identical.  Likewise ceil((X - 0.5) / wX) equals
+// ceil((2X - 1) / (2 wX)) because the quotient can never be an integer.
+struct Axis {
+    int X;        // extent of the axis
+    int wX;       // window size along the axis
+    int shift;    // 1: half-window shift (shifted variant and wX < X)
+    int shifted_variant;
+
+    __host__ __device__ int count() const {
+        if (!shifted_variant) return (X + wX - 1) / wX;
+        if (!shift) return 1;
+        int num = 2 * X - 1, den = 2 * wX;
+        return (num + den - 1) / den + 1;
+    }
+    __host__ __device__ void slice(int i, int* s, int* e) const {
+        if (!shifted_variant) {
+            *s = i * wX;
+            *e = (i + 1) * wX < X ? (i + 1) * wX : X;
+        } else if (!shift) {
+            *s = 0;
+            *e = wX < X ? wX : X;
+        } else {
+            int a = ((2 * i - 1) * wX) / 2;  // truncates toward zero like int()
+            int b = ((2 * i + 1) * wX) / 2;
+            *s = a > 0 ? a : 0;
+            *e = b < X ? b : X;
+        }
+    }
+};
+
+struct GeomParams {
+    Axis ax[3];            // t, h, w
+    int t, h, w;
+    int txt_len;
+    int nwin, sumf;
+    double base[21];       // 1 / 10000^(2j/42), computed on the host in double
+};
+
+// Host plan: sizes, tiles and attention work items.
+struct GeomPlan {
+    int t = 0, h = 0, w = 0, txt_len = 0, nwin = 0, sumf = 0, Lv = 0, max_S = 0;
+    int txt_sets = 1;      // 1: text rows shared by all windows, else nwin
+    int ntt = 0;           // text tiles per set
+    int n_vid_tiles = 0, n_tiles = 0, n_items = 0;
+    bool covers_all = true;  // vidx is a permutation of [0, Lv)
+    std::vector<int32_t> slices;     // nwin*6
+    std::vector<int32_t> cumf;       // nwin+1
+    std::vector<int32_t> tile_base;  // nwin+1, first video tile of window w
+    std::vector<int32_t> tile_win;   // n_vid_tiles, window of each video tile
+    std::vector<int32_t> items;      // n_items*4: window, first q tile, second q tile (-1), 0
+};
+
+}  // namespace awa
+
+struct awa_ctx {
+    int device = 0;
+    std::string err;
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    hipEvent_t ev = nullptr;
+};
+
+struct awa_geom {
+    int device = 0;
+    bool injected = false;
+    awa::GeomPlan plan;
+    int32_t* d_slices = nullptr;
+    int32_t* d_cumf = nullptr;
+    int32_t* d_vidx = nullptr;
+    int32_t* d_tile_base = nullptr;
+    int32_t* d_tile_win = nullptr;
+    int32_t* d_items = nullptr;
+    float* d_vfreq = nullptr;
+    float* d_tfreq = nullptr;
+    float2* d_vcs = nullptr;   // [sumf][63] (cos, sin) per channel pair
+    float2* d_tcs = nullptr;   // [txt_sets*txt_len][63]
+};
+
+namespace awa {
+
+// Kernel launchers (defined in the .hip files).
+hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s);
+hipError_t launch_geom_tables(const float* vfreq, const float* tfreq, int sumf, int trows,
+                              float2* vcs, float2* tcs, hipStream_t s);
+
+struct PackArgs {
+    const void* vqkv;
+    const void* tqkv;
+    const float* nq_v;
+    const float* nk_v;
+    const float* nq_t;
+    const float* nk_t;
+    const int32_t* cumf;
+    const int32_t* vidx;
+    const int32_t* tile_base;
+    const int32_t* tile_win;
+    const float2* vcs;
+    const float2* tcs;
+    void* Qp;
+    void* Kp;
+    void* Vp;
+    int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles;
+    float eps;
+};
+hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s);
+
+struct SdpaArgs {
+    const void* Qp;
+    const void* Kp;
+    const void* Vp;
+    const int32_t* items;
+    const int32_t* cumf;
+    const int32_t* vidx;
+    const int32_t* tile_base;
+    void* vattn;
+    float* tpart;          // [nwin][txt_len][2560] fp32 text partials
+    int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles, n_items, nwin;
+    float scale_log2e;     // (1/sqrt(128)) * log2(e)
+};
+hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s);
+
+hipError_t launch_coalesce(int dtype, const float* tpart, void* tattn, int nwin, int txt_len,
+                           hipStream_t s);
+hipError_t launch_cast_f32_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s);
+hipError_t launch_cast_bf16_f32(const uint16_t* in, float* out, int64_t n, hipStream_t s);
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+
+}  // namespace awa

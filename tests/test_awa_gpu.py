@@ -1,0 +1,268 @@
+"""GPU parity of the AWA op through the C ABI against the oracle.
+
+Bars (from the op's specification):
+  - window and index metadata: bit-exact;
+  - fp32 storage: cos >= 0.99999 and max|d| / max|ref| <= 1e-4 against the
+    reference C++ attention (the oracle, bit-exact to it);
+  - bf16 storage: cos >= 0.9999 against the reference bf16 path, emulated as
+    bf16 inputs widened exactly, fp32 attention, outputs rounded to nearest
+    even (awa_layer.cpp:338-451).
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, metrics, seeded_awa_inputs
+
+pytestmark = pytest.mark.gpu
+
+F32_COS, F32_REL, BF16_COS = 0.99999, 1e-4, 0.9999
+
+CONFIGS = {
+    # name: grid, num_windows, txt, seed, outlier fraction
+    "cfg0_360p": ((1, 23, 27), (4, 3, 3), 58, 0, 0.0),
+    "cfg1_720p": ((1, 45, 53), (4, 3, 3), 58, 1, 0.0),
+    "cfg2_1080p": ((1, 68, 80), (4, 3, 3), 58, 2, 0.0),
+    "cfg4_ragged": ((1, 71, 97), (1, 4, 4), 77, 4, 0.01),
+}
+
+
+def torch_dev():
+    import torch
+    return torch, torch.device("cuda:0")
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("name", list(CONFIGS) + ["edge"])
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_geometry_bit_exact(oracle, ctx, name, shifted):
+    cases = [CONFIGS[name][:3]] if name != "edge" else [
+        ((1, 1, 1), (1, 1, 1), 1), ((2, 3, 4), (2, 40, 40), 3), ((40, 2, 3), (7, 1, 2), 5),
+        ((1, 120, 7), (2, 40, 40), 2), ((3, 5, 7), (4, 3, 3), 70)]
+    for grid, nw, txt in cases:
+        note(f"geometry {grid} {nw} txt={txt} shifted={shifted}")
+        g = ctx.build_geometry(*grid, nw, txt, shifted)
+        d = g.read()
+        o = oracle.Geometry(*grid, nw, txt, shifted)
+        info = g.info()
+        assert info["nwin"] == o.nwin and info["sumf"] == o.sumf and info["Lv"] == o.Lv
+        assert np.array_equal(d["slices"], o.slices)
+        assert np.array_equal(d["cumf"], o.cumf)
+        assert np.array_equal(d["vidx"], o.vidx)
+        assert np.array_equal(d["vid_freq"].view(np.uint32), o.vid_freq.view(np.uint32))
+        assert np.array_equal(d["txt_freq"].view(np.uint32), o.txt_freq.view(np.uint32))
+        g.close()
+
+
+def run_gpu(ctx, geom, vqkv, tqkv, gains, dtype, eps=1e-5):
+    torch, dev = torch_dev()
+    vq = torch.from_numpy(vqkv).to(dev, dtype)
+    tq = torch.from_numpy(tqkv).to(dev, dtype)
+    g4 = [torch.from_numpy(g).to(dev) for g in gains]
+    va, ta = ctx.forward(geom, vq, tq, *g4, eps=eps)
+    torch.cuda.synchronize()
+    return va.float().cpu().numpy(), ta.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["t2_unshifted", "t2_shifted"])
+def test_f32_against_reference_fixture(ctx, name):
+    """fp32 GPU output vs the reference's own stored output."""
+    sys.path.insert(0, os.path.dirname(__file__))
+    from test_oracle_reference import fixture_inputs, load_fixture
+    z, meta = load_fixture(name)
+    vq, tq, gains = fixture_inputs(meta)
+    torch, _ = torch_dev()
+    geom = ctx.build_geometry(*meta["grid"], meta["num_windows"], meta["txt_len"], meta["shifted"])
+    va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.float32, meta["eps"])
+    for out, ref in ((va, z["vattn"]), (ta, z["tattn"])):
+        cos, rel, _ = metrics(out, ref)
+        assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_f32_config0_360p(oracle, ctx, shifted):
+    torch, _ = torch_dev()
+    grid, nw, txt, seed, _ = CONFIGS["cfg0_360p"]
+    note(f"f32 360p shifted={shifted}")
+    vq, tq, gains = seeded_awa_inputs(grid[0] * grid[1] * grid[2], txt, seed)
+    o = oracle.Geometry(*grid, nw, txt, shifted)
+    rv, rt = oracle.awa_forward(vq, tq, o, *gains, eps=1e-5)
+    geom = ctx.build_geometry(*grid, nw, txt, shifted)
+    va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.float32)
+    for out, ref in ((va, rv), (ta, rt)):
+        cos, rel, _ = metrics(out, ref)
+        note(f"  cos={cos:.8f} rel={rel:.2e}")
+        assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
+def bf16_reference(oracle, vq, tq, gains, geom_o):
+    """The reference bf16 path: bf16 in, fp32 attention, bf16 out."""
+    rv, rt = oracle.awa_forward(oracle.bf16_round(vq), oracle.bf16_round(tq), geom_o, *gains, eps=1e-5)
+    return oracle.bf16_round(rv), oracle.bf16_round(rt)
+
+
+@pytest.mark.parametrize("name", ["cfg1_720p", "cfg2_1080p", "cfg4_ragged", "cfg0_360p"])
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_bf16_configs(oracle, ctx, name, shifted):
+    torch, _ = torch_dev()
+    grid, nw, txt, seed, outl = CONFIGS[name]
+    note(f"bf16 {name} shifted={shifted}")
+    vq, tq, gains = seeded_awa_inputs(grid[0] * grid[1] * grid[2], txt, seed, outlier_frac=outl)
+    o = oracle.Geometry(*grid, nw, txt, shifted)
+    rv, rt = bf16_reference(oracle, vq, tq, gains, o)
+    geom = ctx.build_geometry(*grid, nw, txt, shifted)
+    va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.bfloat16)
+    for out, ref in ((va, rv), (ta, rt)):
+        cos, rel, md = metrics(out, ref)
+        note(f"  cos={cos:.8f} rel={rel:.2e} maxd={md:.3e}")
+        assert np.all(np.isfinite(out))
+        assert cos >= BF16_COS, cos
+
+
+def test_f32_on_bf16_config_shapes(oracle, ctx):
+    """The fp32 path at the 1080p shifted shape (25 ragged windows)."""
+    torch, _ = torch_dev()
+    grid, nw, txt, seed, _ = CONFIGS["cfg2_1080p"]
+    vq, tq, gains = seeded_awa_inputs(grid[0] * grid[1] * grid[2], txt, seed)
+    o = oracle.Geometry(*grid, nw, txt, 1)
+    rv, rt = oracle.awa_forward(vq, tq, o, *gains, eps=1e-5)
+    geom = ctx.build_geometry(*grid, nw, txt, 1)
+    va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.float32)
+    for out, ref in ((va, rv), (ta, rt)):
+        cos, rel, _ = metrics(out, ref)
+        assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
+def test_injected_geometry_matches_built(oracle, ctx):
+    """set_window_geometry with the reference's float arrays == device-built."""
+    torch, _ = torch_dev()
+    grid, nw, txt = (1, 23, 27), (4, 3, 3), 58
+    vq, tq, gains = seeded_awa_inputs(grid[1] * grid[2], txt, 7)
+    for shifted in (0, 1):
+        o = oracle.Geometry(*grid, nw, txt, shifted)
+        g_set = ctx.set_geometry(o.vidx.astype(np.float32), o.cumf.astype(np.float32), o.vid_freq,
+                                 o.txt_freq, o.nwin, o.Lv, txt)
+        g_bld = ctx.build_geometry(*grid, nw, txt, shifted)
+        for dt in (torch.float32, torch.bfloat16):
+            a = run_gpu(ctx, g_set, vq, tq, gains, dt)
+            b = run_gpu(ctx, g_bld, vq, tq, gains, dt)
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_partial_cover_zero_fill(oracle, ctx):
+    """Tokens outside every window get zero rows (awa_layer.cpp:386-399)."""
+    torch, _ = torch_dev()
+    o = oracle.Geometry(1, 6, 8, (1, 30, 30), 5, 0)
+    keep = 3  # drop the last windows: their tokens become uncovered
+    cumf = o.cumf[: keep + 1]
+    vidx = o.vidx[: cumf[-1]]
+    vq, tq, gains = seeded_awa_inputs(o.Lv, 5, 8)
+    g = ctx.set_geometry(vidx.astype(np.float32), cumf.astype(np.float32), o.vid_freq[: cumf[-1]],
+                         o.txt_freq[: keep * 5], keep, o.Lv, 5)
+    torch_, dev = torch_dev()
+    out = torch_.full((o.Lv, 2560), 7.0, device=dev)
+    tout = torch_.empty((5, 2560), device=dev)
+    ctx.forward(g, torch_.from_numpy(vq).to(dev), torch_.from_numpy(tq).to(dev),
+                *[torch_.from_numpy(x).to(dev) for x in gains], vattn=out, tattn=tout)
+    torch_.cuda.synchronize()
+    va = out.cpu().numpy()
+    covered = np.zeros(o.Lv, bool)
+    covered[vidx] = True
+    assert np.all(va[~covered] == 0.0)
+    # the covered rows equal the oracle run on the same partial geometry
+    import types
+    og = types.SimpleNamespace(t=1, h=6, w=8, Lv=o.Lv, txt_len=5, slices=np.ascontiguousarray(o.slices[:keep]),
+                               nwin=keep, vid_freq=np.ascontiguousarray(o.vid_freq[: cumf[-1]]),
+                               txt_freq=np.ascontiguousarray(o.txt_freq[: keep * 5]))
+    rv, rt = oracle.awa_forward(vq, tq, og, *gains, eps=1e-5)
+    cos, rel, _ = metrics(va[covered], rv[covered])
+    assert cos >= F32_COS and rel <= F32_REL
+    cos, rel, _ = metrics(tout.cpu().numpy(), rt)
+    assert cos >= F32_COS and rel <= F32_REL
+
+
+def test_single_window_is_plain_attention(oracle, ctx):
+    """num_windows (1,1,1) on a small grid: one window, so the op is ordinary
+    softmax attention over Lv + TXT rows of normalised, rotated q/k (checked
+    in fp64 with torch's SDPA on the CPU)."""
+    import torch
+    o = oracle.Geometry(1, 5, 7, (1, 1, 1), 6, 0)
+    assert o.nwin == 1
+    vq, tq, gains = seeded_awa_inputs(o.Lv, 6, 9)
+    g = ctx.build_geometry(1, 5, 7, (1, 1, 1), 6, 0)
+    va, ta = run_gpu(ctx, g, vq, tq, gains, torch.float32)
+    # fp64 reference built from the oracle's per-token ops
+    rows = [(vq[tok], gains[0], gains[1], o.vid_freq[r]) for r, tok in enumerate(o.vidx)]
+    rows += [(tq[i], gains[2], gains[3], o.txt_freq[i]) for i in range(6)]
+    Q, K, V = [], [], []
+    for x, gq, gk, fr in rows:
+        qn = oracle.qk_norm(x[:2560], gq).reshape(20, 128)
+        kn = oracle.qk_norm(x[2560:5120], gk).reshape(20, 128)
+        Q.append(np.stack([oracle.apply_rope(fr, qn[h]) for h in range(20)]))
+        K.append(np.stack([oracle.apply_rope(fr, kn[h]) for h in range(20)]))
+        V.append(x[5120:].reshape(20, 128))
+    Q, K, V = (torch.from_numpy(np.stack(a).transpose(1, 0, 2).astype(np.float64)) for a in (Q, K, V))
+    O_ = torch.nn.functional.scaled_dot_product_attention(Q, K, V).numpy().transpose(1, 0, 2).reshape(-1, 2560)
+    ref_v = np.zeros_like(va)
+    ref_v[o.vidx] = O_[: o.Lv]
+    for out, ref in ((va, ref_v), (ta, O_[o.Lv:])):
+        cos, rel, _ = metrics(out, ref)
+        assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
+def test_forward_host_matches_device(oracle, ctx):
+    """AwaVk-style host-vector entry == the device entry (fp32)."""
+    torch, _ = torch_dev()
+    vq, tq, gains = seeded_awa_inputs(6 * 8, 5, 10)
+    g = ctx.build_geometry(1, 6, 8, (1, 30, 30), 5, 1)
+    hv, ht = ctx.forward_host(g, vq, tq, *gains)
+    dv, dt = run_gpu(ctx, g, vq, tq, gains, torch.float32)
+    assert np.array_equal(hv, dv) and np.array_equal(ht, dt)
+
+
+def test_deterministic(ctx):
+    torch, _ = torch_dev()
+    vq, tq, gains = seeded_awa_inputs(68 * 80, 58, 2)
+    g = ctx.build_geometry(1, 68, 80, (4, 3, 3), 58, 1)
+    a = run_gpu(ctx, g, vq, tq, gains, torch.bfloat16)
+    b = run_gpu(ctx, g, vq, tq, gains, torch.bfloat16)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_error_paths(oracle, ctx, awa):
+    """Bad shapes and geometry return AWA_EARG with a message; no kernel runs."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = ctx.build_geometry(1, 6, 8, (1, 30, 30), 5, 0)
+    vq = torch.zeros((48, 7680), device=dev)
+    tq = torch.zeros((5, 7680), device=dev)
+    gn = [torch.ones(128, device=dev) for _ in range(4)]
+    with pytest.raises(awa.AwaError) as e:
+        ctx.forward(g, torch.zeros((47, 7680), device=dev), tq, *gn)
+    assert e.value.code == awa.AWA_EARG and "Lv" in str(e.value)
+    with pytest.raises(awa.AwaError):
+        ctx.forward(g, vq, torch.zeros((4, 7680), device=dev), *gn)
+    with pytest.raises(awa.AwaError):
+        ctx.forward(g, vq, tq, *gn, eps=0.0)
+    with pytest.raises(awa.AwaError):
+        ctx.build_geometry(0, 6, 8, (1, 1, 1), 5, 0)
+    o = oracle.Geometry(1, 6, 8, (1, 30, 30), 5, 0)
+    bad = o.vidx.astype(np.float32).copy()
+    bad[1] = bad[0]  # a token in two windows
+    with pytest.raises(awa.AwaError):
+        ctx.set_geometry(bad, o.cumf.astype(np.float32), o.vid_freq, o.txt_freq, o.nwin, o.Lv, 5)
+    bad = o.vidx.astype(np.float32).copy()
+    bad[0] = o.Lv  # outside the grid
+    with pytest.raises(awa.AwaError):
+        ctx.set_geometry(bad, o.cumf.astype(np.float32), o.vid_freq, o.txt_freq, o.nwin, o.Lv, 5)
+    vf = o.vid_freq.copy()
+    vf[0, 1] += 1.0  # channel pair no longer repeated
+    with pytest.raises(awa.AwaError):
+        ctx.set_geometry(o.vidx.astype(np.float32), o.cumf.astype(np.float32), vf, o.txt_freq, o.nwin, o.Lv, 5)
