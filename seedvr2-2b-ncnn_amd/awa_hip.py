@@ -45,6 +45,11 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is missing: build it (make -C {HERE}) before use")
+        # torch ships its own HIP runtime with the same soname
+        # (libamdhip64.so.7).  Load it first so the library binds to that one
+        # runtime instead of starting a second one from /opt/rocm in the same
+        # process: torch's tensors and streams then belong to our runtime too.
+        import torch  # noqa: F401
         L = C.CDLL(LIB_PATH)
         vp, i32p, f32p = C.c_void_p, C.POINTER(C.c_int32), C.POINTER(C.c_float)
         L.awa_create.argtypes = [C.POINTER(vp), C.c_int]
