@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Benchmark: the SeedVR2 AWA layer at the 1080p shape, bf16, one MI355X.
+
+A step is one AWA layer forward (qk-norm + RoPE + window partition, window
+attention, cross-window text average) on resident inputs: vqkv [5440, 7680]
+and tqkv [58, 7680] bf16 for the 1x68x80 token grid, 20 heads x 128, 58 text
+tokens, num_windows (4,3,3).  Steps alternate the unshifted (16 windows) and
+shifted (25 windows) geometry, as even and odd DiT layers do; geometry is
+built once per resolution before timing, as the reference caches it.
+
+Prints one JSON line.  `value` is ms per AWA layer (wall clock over the
+timed steps, bracketed by device synchronisation).  `roofline` covers the
+dominant kernel (window attention) from HIP events recorded on its stream
+during the timed steps.  `cpu_baseline` times the oracle's single-threaded
+restatement of the reference CPU attention (dit_vk.cpp:345-462) on one full
+unshifted 1080p layer.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "seedvr2-2b-ncnn_amd"))
+
+METRIC = "1080p bf16 AWA-layer ms & MFMA util; 32-layer DiT step sec; 1 GPU"
+GRID, NUM_WINDOWS, TXT, SEED = (1, 68, 80), (4, 3, 3), 58, 2
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def sdpa_flops(S_list):
+    # QK^T + PV over each window's S = f + TXT rows, 20 heads x 128
+    return sum(4.0 * 128 * 20 * s * s for s in S_list)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(vq_bf16_f32, tq_bf16_f32, gains):
+    """Single-threaded oracle (bit-exact restatement of the reference CPU AWA)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    g = O.Geometry(*GRID, NUM_WINDOWS, TXT, 0)
+    t0 = time.perf_counter()
+    O.awa_forward(vq_bf16_f32, tq_bf16_f32, g, *gains, eps=1e-5, nthreads=1)
+    dt = time.perf_counter() - t0
+    return {"value": round(dt * 1e3, 1), "unit": "ms per AWA layer", "cores": 1, "kind": "port",
+            "sample": "one full 1080p unshifted AWA layer (16 windows, fp32 CPU attention of "
+                      "dit_vk.cpp:345-462 via the bit-exact oracle), single thread",
+            "cpu": cpu_model(), "nproc": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="only run a plain device copy of MB MiB (4 times) to calibrate the "
+                         "FETCH_SIZE/WRITE_SIZE counters, then exit")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the AWA path is single-GPU here (no sharding, no "
+              "collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": n * 4, "launches": 4}))
+        return
+
+    import awa_hip
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(SEED)
+    Lv = GRID[0] * GRID[1] * GRID[2]
+    vq = torch.from_numpy(rng.standard_normal((Lv, 7680), dtype=np.float32)).to(dev, torch.bfloat16)
+    tq = torch.from_numpy(rng.standard_normal((TXT, 7680), dtype=np.float32)).to(dev, torch.bfloat16)
+    gains_np = [(1.0 + 0.02 * rng.standard_normal(128)).astype(np.float32) for _ in range(4)]
+    gains = [torch.from_numpy(g).to(dev) for g in gains_np]
+    vattn = torch.empty((Lv, 2560), dtype=torch.bfloat16, device=dev)
+    tattn = torch.empty((TXT, 2560), dtype=torch.bfloat16, device=dev)
+
+    ctx = awa_hip.Context(0)
+    geoms = [ctx.build_geometry(*GRID, NUM_WINDOWS, TXT, sh) for sh in (0, 1)]
+    infos = [g.info() for g in geoms]
+    S_lists = []
+    for g in geoms:
+        d = g.read()
+        S_lists.append([int(c1 - c0) + TXT for c0, c1 in zip(d["cumf"][:-1], d["cumf"][1:])])
+    flops = [sdpa_flops(S) for S in S_lists]
+
+    def step(k):
+        ctx.forward(geoms[k % 2], vq, tq, *gains, eps=1e-5, vattn=vattn, tattn=tattn)
+
+    for k in range(args.warmup):
+        step(k)
+    torch.cuda.synchronize()
+    ctx.timing(True)
+    ctx.timing_read()  # clear
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(k)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_pack, ms_attn, ms_text, calls = ctx.timing_read()
+    ctx.timing(False)
+    assert calls == args.steps
+    ms_step = (t1 - t0) * 1e3 / args.steps
+
+    # per-variant breakdown (separate short runs, events only)
+    per_variant = {}
+    for sh, name in ((0, "unshifted"), (1, "shifted")):
+        ctx.timing(True)
+        ctx.timing_read()
+        n = max(4, args.steps // 2)
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        for _ in range(n):
+            ctx.forward(geoms[sh], vq, tq, *gains, eps=1e-5, vattn=vattn, tattn=tattn)
+        torch.cuda.synchronize()
+        b = time.perf_counter()
+        p, s_, t_, c = ctx.timing_read()
+        ctx.timing(False)
+        per_variant[name] = {"layer_ms": round((b - a) * 1e3 / n, 4), "pack_us": round(p / c * 1e3, 2),
+                             "attn_us": round(s_ / c * 1e3, 2), "text_avg_us": round(t_ / c * 1e3, 2),
+                             "attn_tflops": round(flops[sh] / (s_ / c * 1e-3) / 1e12, 1),
+                             "nwin": infos[sh]["nwin"]}
+
+    # roofline of the dominant kernel (window attention) over the timed steps
+    n_unsh = (args.steps + 1) // 2
+    n_sh = args.steps // 2
+    flops_timed = n_unsh * flops[0] + n_sh * flops[1]
+    attn_avg_s = ms_attn * 1e-3 / calls
+    achieved = flops_timed / calls / attn_avg_s / 1e12
+    # memory-bound pass: qk-norm + RoPE, algorithmic bytes = read + write q and k
+    qk_bytes = 2 * (Lv + TXT) * 2 * 2560 * 2
+    pack_avg_s = ms_pack * 1e-3 / calls
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_step, 4),
+        "unit": "ms per AWA layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q/k/v ~ N(0,1), gains 1+N(0,0.02), seed 2)",
+        "config": {"workload": "awa_layer_1080p_bf16", "grid": list(GRID), "txt_len": TXT,
+                   "heads": 20, "head_dim": 128, "num_windows": list(NUM_WINDOWS),
+                   "steps_alternate": "unshifted (16 windows) / shifted (25 windows)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel": "sdpa_bf16_kernel",
+                     "avg_launch_us": round(attn_avg_s * 1e6, 2),
+                     "algorithmic_gflop_per_launch": round(flops_timed / calls / 1e9, 3)},
+        "phases_us": {"pack_qknorm_rope": round(pack_avg_s * 1e6, 2),
+                      "attention": round(attn_avg_s * 1e6, 2),
+                      "text_average": round(ms_text * 1e3 / calls, 2)},
+        "hbm_qknorm_rope": {"algorithmic_bytes": qk_bytes,
+                            "achieved_GBs": round(qk_bytes / pack_avg_s / 1e9, 1),
+                            "frac": round(qk_bytes / pack_avg_s / 1e9 / PEAK_HBM_GBS, 4)},
+        "per_variant": per_variant,
+    }
+    if not args.no_cpu_baseline:
+        vqf = vq.float().cpu().numpy()
+        tqf = tq.float().cpu().numpy()
+        out["cpu_baseline"] = cpu_baseline(vqf, tqf, gains_np)
+    for g in geoms:
+        g.close()
+    ctx.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -128,6 +128,15 @@ int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv,
                      const float* h_nk_v, const float* h_nq_t, const float* h_nk_t,
                      float eps, float* h_vid_out, float* h_txt_out);
 
+/* Per-phase device timing, the MI355X counterpart of the reference's
+ * [perf] accumulators (dit_vk.cpp:23-24, 332-334) at kernel granularity.
+ * While enabled, every awa_forward records HIP events on its stream around
+ * the pack (qk-norm + RoPE + partition), attention and text-average kernels.
+ * awa_timing_read waits for the recorded events, returns the summed
+ * milliseconds of each phase and the number of calls, and clears them. */
+int awa_timing_enable(awa_ctx* ctx, int enable);
+int awa_timing_read(awa_ctx* ctx, double* ms_pack, double* ms_attn, double* ms_text, int* calls);
+
 /* Casts at the bf16 boundary (cast_f32_bf16.comp:23-24, round to nearest
  * even; cast_bf16_f32.comp:18-19, exact widening).  n elements. */
 int awa_cast_f32_to_bf16(awa_ctx* ctx, const float* d_in, uint16_t* d_out, int64_t n,

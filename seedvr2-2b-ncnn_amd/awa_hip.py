@@ -70,6 +70,9 @@ def lib():
                                   C.c_float, vp, vp, vp]
         L.awa_forward_host.argtypes = [vp, vp, f32p, f32p, C.c_int, C.c_int, f32p, f32p, f32p, f32p,
                                        C.c_float, f32p, f32p]
+        L.awa_timing_enable.argtypes = [vp, C.c_int]
+        L.awa_timing_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                      C.POINTER(C.c_double), C.POINTER(C.c_int)]
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
@@ -137,6 +140,18 @@ class Context:
             self.close()
         except Exception:
             pass
+
+    # ---- timing
+    def timing(self, enable=True):
+        self.check(lib().awa_timing_enable(self.ptr, int(bool(enable))), "awa_timing_enable")
+
+    def timing_read(self):
+        """Summed per-phase ms since the last read: (pack, attention, text, calls)."""
+        a, b, c = C.c_double(), C.c_double(), C.c_double()
+        n = C.c_int()
+        self.check(lib().awa_timing_read(self.ptr, C.byref(a), C.byref(b), C.byref(c), C.byref(n)),
+                   "awa_timing_read")
+        return a.value, b.value, c.value, n.value
 
     # ---- geometry
     def build_geometry(self, t, h, w, num_windows, txt_len, shifted, stream=None):

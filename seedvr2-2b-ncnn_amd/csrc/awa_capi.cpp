@@ -187,6 +187,20 @@ int ensure_scratch(awa_ctx* ctx, size_t bytes) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+hipError_t timing_mark(awa_ctx* ctx, hipStream_t s) {
+    if (!ctx->timing) return hipSuccess;
+    hipEvent_t e;
+    if (!ctx->ev_free.empty()) {
+        e = ctx->ev_free.back();
+        ctx->ev_free.pop_back();
+    } else {
+        hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) return r;
+    }
+    ctx->ev_used.push_back(e);
+    return hipEventRecord(e, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -207,6 +221,8 @@ void awa_destroy(awa_ctx* ctx) {
     if (!ctx) return;
     DeviceGuard dg(ctx->device);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    for (hipEvent_t e : ctx->ev_free) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->ev_used) (void)hipEventDestroy(e);
     delete ctx;
 }
 
@@ -493,6 +509,7 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, 
     char* base = static_cast<char*>(ctx->scratch);
 
     if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
+    HIPCK(ctx, timing_mark(ctx, s));
 
     PackArgs pa{};
     pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
@@ -503,6 +520,7 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, 
     pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
     pa.n_tiles = P.n_tiles; pa.eps = eps;
     HIPCK(ctx, launch_pack(dtype, pa, s));
+    HIPCK(ctx, timing_mark(ctx, s));
 
     SdpaArgs sa{};
     sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
@@ -512,8 +530,10 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, 
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
     sa.scale_log2e = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
     HIPCK(ctx, launch_sdpa(dtype, sa, s));
+    HIPCK(ctx, timing_mark(ctx, s));
 
     HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
+    HIPCK(ctx, timing_mark(ctx, s));
     return AWA_OK;
 }
 
@@ -565,6 +585,40 @@ int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv, const
     cp(h_vid_out, dvo, ov * 4, hipMemcpyDeviceToHost);
     cp(h_txt_out, dto, ot * 4, hipMemcpyDeviceToHost);
     (void)hipFree(buf);
+    return rc;
+}
+
+int awa_timing_enable(awa_ctx* ctx, int enable) {
+    if (!ctx) return AWA_EARG;
+    ctx->timing = enable != 0;
+    return AWA_OK;
+}
+
+int awa_timing_read(awa_ctx* ctx, double* ms_pack, double* ms_attn, double* ms_text, int* calls) {
+    if (!ctx) return AWA_EARG;
+    DeviceGuard dg(ctx->device);
+    double acc[3] = {0, 0, 0};
+    const size_t n = ctx->ev_used.size() / 4;
+    int rc = AWA_OK;
+    for (size_t i = 0; i < n && rc == AWA_OK; i++) {
+        hipEvent_t* e = &ctx->ev_used[4 * i];
+        hipError_t r = hipEventSynchronize(e[3]);
+        for (int k = 0; k < 3 && r == hipSuccess; k++) {
+            float ms = 0.f;
+            r = hipEventElapsedTime(&ms, e[k], e[k + 1]);
+            acc[k] += ms;
+        }
+        if (r != hipSuccess) {
+            set_err(ctx, "awa_timing_read: %s", hipGetErrorString(r));
+            rc = AWA_EHIP;
+        }
+    }
+    ctx->ev_free.insert(ctx->ev_free.end(), ctx->ev_used.begin(), ctx->ev_used.end());
+    ctx->ev_used.clear();
+    if (ms_pack) *ms_pack = acc[0];
+    if (ms_attn) *ms_attn = acc[1];
+    if (ms_text) *ms_text = acc[2];
+    if (calls) *calls = (int)n;
     return rc;
 }
 

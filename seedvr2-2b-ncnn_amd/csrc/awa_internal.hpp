@@ -89,7 +89,11 @@ struct awa_ctx {
     std::string err;
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
-    hipEvent_t ev = nullptr;
+    // Per-phase timing (awa_timing_enable): 4 events per recorded call,
+    // bracketing pack, attention and text average on the call's stream.
+    bool timing = false;
+    std::vector<hipEvent_t> ev_free;
+    std::vector<hipEvent_t> ev_used;
 };
 
 struct awa_geom {
