@@ -1,0 +1,96 @@
+/*
+ * dit_capi.h — C ABI of the DiT block around the AWA op on MI355X (gfx950).
+ *
+ * Replaces the per-layer body of DitVk::forward_latent (src/dit_vk.cpp:517-632)
+ * with DitVk::awa_forward (dit_vk.cpp:312-463) and swiglu (dit_vk.cpp:465-472),
+ * the AdaCompose layer (src/ada_compose.cpp:165-235) and time_embedding
+ * (dit_vk.cpp:295-309), in the order of the merged graph
+ * (export/export_dit_graph.py:155-226):
+ *
+ *   h   = RMSNorm(x) * (emb[6d+1] + attn_scale) + (emb[6d] + attn_shift)
+ *   qkv = h W_qkv^T                                   (no bias)
+ *   a   = AWA(qkv_vid, qkv_txt)                       (awa_capi.h)
+ *   x  += (a W_out^T + b_out) * (emb[6d+2] + attn_gate)
+ *   h   = RMSNorm(x) * (emb[6d+4] + mlp_scale) + (emb[6d+3] + mlp_shift)
+ *   x  += ((silu(h W_gate^T) * (h W_in^T)) W_mlp_out^T) * (emb[6d+5] + mlp_gate)
+ *
+ * for the video rows with the video branch and the text rows with the text
+ * branch (the two branches are the same weights from layer 10 on).  With
+ * txt_vid_only set (forward_latent's last layer, dit_vk.cpp:523-620) the text
+ * rows get no ada modulation before attention, no attention gate and no MLP.
+ *
+ * Precision: weights and GEMM inputs bf16, fp32 accumulation on the matrix
+ * cores, fp32 residual stream x, bf16 AWA boundary as AwaLayer's.
+ *
+ * Conventions as awa_capi.h: device pointers, stream-ordered, 0 / AWA_EARG /
+ * AWA_EHIP, messages through awa_last_error of the context.
+ */
+#ifndef SEEDVR2_DIT_CAPI_H
+#define SEEDVR2_DIT_CAPI_H
+
+#include <stdint.h>
+
+#include "awa_capi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { DIT_MLP = 6912, DIT_EMB = 15360 };
+
+/* One branch's weights on the device (names as the reference's per-branch
+ * files, dit_vk.cpp:163-177 and verify_dit.cpp:163-179). */
+typedef struct {
+    const uint16_t* qkv_w;      /* bf16 [7680][2560]                              */
+    const uint16_t* out_w;      /* bf16 [2560][2560]                              */
+    const float* out_b;         /* fp32 [2560]                                    */
+    const uint16_t* mlp_w;      /* bf16 [2*mlp][2560], from dit_pack_mlp_weights  */
+    const uint16_t* mlp_out_w;  /* bf16 [2560][mlp]                               */
+    const float* nq;            /* fp32 [128] qk-norm gains                       */
+    const float* nk;
+    const float* attn_shift;    /* fp32 [2560] each                               */
+    const float* attn_scale;
+    const float* attn_gate;
+    const float* mlp_shift;
+    const float* mlp_scale;
+    const float* mlp_gate;
+} dit_branch;
+
+/* Interleaves proj_in (w_in) and proj_in_gate (w_gate), each bf16 [mlp][2560],
+ * into the fused SwiGLU weight [2*mlp][2560]: 32-row blocks alternate
+ * in, gate, in, gate, ... (mlp a multiple of 128). */
+int dit_pack_mlp_weights(awa_ctx* ctx, const uint16_t* d_w_in, const uint16_t* d_w_gate,
+                         int mlp, uint16_t* d_w_cat, awa_stream_t stream);
+
+/* time_embedding(t) (dit_vk.cpp:295-309): 256-wide sinusoid (sin half, then
+ * cos), then Linear 256->2560, SiLU, Linear 2560->2560, SiLU,
+ * Linear 2560->15360, fp32 weights [out][in] and biases; d_emb fp32 [15360]. */
+int dit_time_embedding(awa_ctx* ctx, float t, const float* d_w_in, const float* d_b_in,
+                       const float* d_w_hid, const float* d_b_hid, const float* d_w_out,
+                       const float* d_b_out, float* d_emb, awa_stream_t stream);
+
+/* One DiT layer in place on the residual stream d_x, fp32 [Lv + TXT][2560]
+ * (video rows first, then the text rows).  g is the layer's window geometry
+ * (unshifted on even layers, shifted on odd ones, dit_vk.cpp:518).  vb / tb
+ * are the video and text branches (the same pointer for shared layers).
+ * d_emb is the timestep embedding [15360].  mlp is the SwiGLU width (6912 in
+ * the reference checkpoint).  Scratch comes from the context. */
+int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb,
+                      const dit_branch* tb, const float* d_emb, int mlp, int txt_vid_only,
+                      float eps, float* d_x, int Lv, int TXT, awa_stream_t stream);
+
+/* Per-phase device timing of dit_layer_forward (HIP events on its stream):
+ * GEMMs, AWA op, and norms/elementwise, summed since the last read. */
+int dit_timing_read(awa_ctx* ctx, double* ms_gemm, double* ms_awa, double* ms_eltwise,
+                    int* layers);
+
+/* Plain bf16 GEMM with the block's kernel, for tests and measurement:
+ * C[M][N] = A[M][K] W[N][K]^T, bf16 in, bf16 out (fp32 accumulation).
+ * N a multiple of 256, K a multiple of 64. */
+int dit_gemm_bf16(awa_ctx* ctx, const uint16_t* d_A, const uint16_t* d_W, uint16_t* d_C, int M,
+                  int N, int K, awa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

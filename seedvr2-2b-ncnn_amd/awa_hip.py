@@ -29,6 +29,15 @@ class AwaError(RuntimeError):
         self.code = code
 
 
+BRANCH_FIELDS = ("qkv_w", "out_w", "out_b", "mlp_w", "mlp_out_w", "nq", "nk", "attn_shift",
+                 "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate")
+
+
+class DitBranch(C.Structure):
+    """dit_branch of include/dit_capi.h (device pointers)."""
+    _fields_ = [(n, C.c_void_p) for n in BRANCH_FIELDS]
+
+
 class GeomInfo(C.Structure):
     _fields_ = [(n, C.c_int32) for n in
                 ("t", "h", "w", "nwin", "sumf", "Lv", "txt_len", "max_S", "n_tiles", "n_items")]
@@ -73,6 +82,13 @@ def lib():
         L.awa_timing_enable.argtypes = [vp, C.c_int]
         L.awa_timing_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                       C.POINTER(C.c_double), C.POINTER(C.c_int)]
+        L.dit_pack_mlp_weights.argtypes = [vp, vp, vp, C.c_int, vp, vp]
+        L.dit_time_embedding.argtypes = [vp, C.c_float, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.dit_layer_forward.argtypes = [vp, vp, C.POINTER(DitBranch), C.POINTER(DitBranch), vp, C.c_int,
+                                        C.c_int, C.c_float, vp, C.c_int, C.c_int, vp]
+        L.dit_timing_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                      C.POINTER(C.c_double), C.POINTER(C.c_int)]
+        L.dit_gemm_bf16.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
@@ -204,6 +220,57 @@ class Context:
         self.check(rc, "awa_forward")
         self._keep = gains  # alive until the stream consumed them
         return vattn, tattn
+
+    # ---- the DiT block (include/dit_capi.h)
+    def gemm(self, A, W, out=None, stream=None):
+        """C = A W^T, bf16 [M,K] x [N,K] -> [M,N] bf16 (the block's GEMM kernel)."""
+        import torch
+        M, K = A.shape
+        N = W.shape[0]
+        if out is None:
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+        rc = lib().dit_gemm_bf16(self.ptr, C.c_void_p(A.data_ptr()), C.c_void_p(W.data_ptr()),
+                                 C.c_void_p(out.data_ptr()), M, N, K, _stream_ptr(stream))
+        self.check(rc, "dit_gemm_bf16")
+        return out
+
+    def pack_mlp(self, w_in, w_gate, stream=None):
+        import torch
+        mlp = w_in.shape[0]
+        out = torch.empty((2 * mlp, w_in.shape[1]), dtype=torch.bfloat16, device=w_in.device)
+        rc = lib().dit_pack_mlp_weights(self.ptr, C.c_void_p(w_in.data_ptr()), C.c_void_p(w_gate.data_ptr()),
+                                        mlp, C.c_void_p(out.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_pack_mlp_weights")
+        return out
+
+    def time_embedding(self, t, w_in, b_in, w_hid, b_hid, w_out, b_out, stream=None):
+        import torch
+        emb = torch.empty(15360, dtype=torch.float32, device=w_in.device)
+        ts = (w_in, b_in, w_hid, b_hid, w_out, b_out)
+        rc = lib().dit_time_embedding(self.ptr, float(t), *[C.c_void_p(x.data_ptr()) for x in ts],
+                                      C.c_void_p(emb.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_time_embedding")
+        return emb
+
+    def layer(self, geom, vbranch, tbranch, emb, x, Lv, TXT, mlp=6912, txt_vid_only=False, eps=1e-5,
+              stream=None):
+        """dit_layer_forward in place on x (fp32 [Lv+TXT, 2560]).  Branches are dicts of
+        device tensors keyed like dit_branch; pass the same dict for shared layers."""
+        vb = DitBranch(**{k: vbranch[k].data_ptr() for k in BRANCH_FIELDS})
+        tb = vb if tbranch is vbranch else DitBranch(**{k: tbranch[k].data_ptr() for k in BRANCH_FIELDS})
+        rc = lib().dit_layer_forward(self.ptr, geom.ptr, C.byref(vb), C.byref(tb),
+                                     C.c_void_p(emb.data_ptr()), int(mlp), int(bool(txt_vid_only)),
+                                     float(eps), C.c_void_p(x.data_ptr()), int(Lv), int(TXT),
+                                     _stream_ptr(stream))
+        self.check(rc, "dit_layer_forward")
+        return x
+
+    def dit_timing_read(self):
+        a, b, c = C.c_double(), C.c_double(), C.c_double()
+        n = C.c_int()
+        self.check(lib().dit_timing_read(self.ptr, C.byref(a), C.byref(b), C.byref(c), C.byref(n)),
+                   "dit_timing_read")
+        return a.value, b.value, c.value, n.value
 
     def forward_host(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, eps=1e-5):
         """AwaVk::forward: numpy fp32 in and out, synchronous."""

@@ -15,7 +15,7 @@
 
 using namespace awa;
 
-namespace {
+namespace awa {
 
 void set_err(awa_ctx* ctx, const char* fmt, ...) {
     if (!ctx) return;
@@ -27,19 +27,46 @@ void set_err(awa_ctx* ctx, const char* fmt, ...) {
     ctx->err = buf;
 }
 
-// Makes ctx->device current for the scope and restores the caller's device.
-struct DeviceGuard {
-    int prev = -1;
-    bool ok = false;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        ok = (prev == dev) || (hipSetDevice(dev) == hipSuccess);
+// Makes the given device current for the scope and restores the caller's.
+DeviceGuard::DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = (prev == dev) || (hipSetDevice(dev) == hipSuccess);
+}
+DeviceGuard::~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+}
+
+hipError_t ensure_buffer(void** buf, size_t* have, size_t need) {
+    if (*have >= need) return hipSuccess;
+    if (*buf) {
+        hipError_t e = hipFree(*buf);
+        *buf = nullptr;
+        *have = 0;
+        if (e != hipSuccess) return e;
     }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    hipError_t e = hipMalloc(buf, need);
+    if (e == hipSuccess) *have = need;
+    return e;
+}
+
+hipError_t event_mark(awa_ctx* ctx, std::vector<hipEvent_t>& list, hipStream_t s) {
+    if (!ctx->timing) return hipSuccess;
+    hipEvent_t e;
+    if (!ctx->ev_free.empty()) {
+        e = ctx->ev_free.back();
+        ctx->ev_free.pop_back();
+    } else {
+        hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) return r;
     }
-};
+    list.push_back(e);
+    return hipEventRecord(e, s);
+}
+
+}  // namespace awa
+
+namespace {
 
 #define HIPCK(ctx, expr)                                                                     \
     do {                                                                                     \
@@ -173,35 +200,61 @@ int plan_axes(int t, int h, int w, const int32_t num_windows[3], int shifted, Ge
 size_t elem_size(int dtype) { return dtype == AWA_BF16 ? 2 : 4; }
 
 int ensure_scratch(awa_ctx* ctx, size_t bytes) {
-    if (ctx->scratch_bytes >= bytes) return AWA_OK;
-    if (ctx->scratch) {
-        // hipFree waits for work still using the old buffer.
-        HIPCK(ctx, hipFree(ctx->scratch));
-        ctx->scratch = nullptr;
-        ctx->scratch_bytes = 0;
-    }
-    HIPCK(ctx, hipMalloc(&ctx->scratch, bytes));
-    ctx->scratch_bytes = bytes;
+    HIPCK(ctx, ensure_buffer(&ctx->scratch, &ctx->scratch_bytes, bytes));
     return AWA_OK;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-hipError_t timing_mark(awa_ctx* ctx, hipStream_t s) {
-    if (!ctx->timing) return hipSuccess;
-    hipEvent_t e;
-    if (!ctx->ev_free.empty()) {
-        e = ctx->ev_free.back();
-        ctx->ev_free.pop_back();
-    } else {
-        hipError_t r = hipEventCreate(&e);
-        if (r != hipSuccess) return r;
-    }
-    ctx->ev_used.push_back(e);
-    return hipEventRecord(e, s);
-}
+hipError_t timing_mark(awa_ctx* ctx, hipStream_t s) { return event_mark(ctx, ctx->ev_used, s); }
 
 }  // namespace
+
+namespace awa {
+
+int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
+                 const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
+                 float eps, void* d_vattn, void* d_tattn, hipStream_t s) {
+    const GeomPlan& P = g->plan;
+    const int Lv = P.Lv;
+    const size_t es = elem_size(dtype);
+    const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
+    const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
+    const size_t tpart_bytes = (size_t)P.nwin * P.txt_len * DIM * 4;
+    int rc = ensure_scratch(ctx, off_t + align256(tpart_bytes));
+    if (rc != AWA_OK) return rc;
+    char* base = static_cast<char*>(ctx->scratch);
+
+    if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
+    HIPCK(ctx, timing_mark(ctx, s));
+
+    PackArgs pa{};
+    pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
+    pa.nq_v = d_nq_v; pa.nk_v = d_nk_v; pa.nq_t = d_nq_t; pa.nk_t = d_nk_t;
+    pa.cumf = g->d_cumf; pa.vidx = g->d_vidx; pa.tile_base = g->d_tile_base; pa.tile_win = g->d_tile_win;
+    pa.vcs = g->d_vcs; pa.tcs = g->d_tcs;
+    pa.Qp = base; pa.Kp = base + off_k; pa.Vp = base + off_v;
+    pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
+    pa.n_tiles = P.n_tiles; pa.eps = eps;
+    HIPCK(ctx, launch_pack(dtype, pa, s));
+    HIPCK(ctx, timing_mark(ctx, s));
+
+    SdpaArgs sa{};
+    sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
+    sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
+    sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
+    sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
+    sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
+    sa.scale_log2e = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
+    HIPCK(ctx, launch_sdpa(dtype, sa, s));
+    HIPCK(ctx, timing_mark(ctx, s));
+
+    HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
+    HIPCK(ctx, timing_mark(ctx, s));
+    return AWA_OK;
+}
+
+}  // namespace awa
 
 extern "C" {
 
@@ -221,8 +274,11 @@ void awa_destroy(awa_ctx* ctx) {
     if (!ctx) return;
     DeviceGuard dg(ctx->device);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->small) (void)hipFree(ctx->small);
     for (hipEvent_t e : ctx->ev_free) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->ev_used) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->dit_ev_used) (void)hipEventDestroy(e);
     delete ctx;
 }
 
@@ -499,42 +555,8 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, 
         return AWA_EARG;
     }
     DeviceGuard dg(ctx->device);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const size_t es = elem_size(dtype);
-    const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
-    const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
-    const size_t tpart_bytes = (size_t)P.nwin * P.txt_len * DIM * 4;
-    int rc = ensure_scratch(ctx, off_t + align256(tpart_bytes));
-    if (rc != AWA_OK) return rc;
-    char* base = static_cast<char*>(ctx->scratch);
-
-    if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
-    HIPCK(ctx, timing_mark(ctx, s));
-
-    PackArgs pa{};
-    pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
-    pa.nq_v = d_nq_v; pa.nk_v = d_nk_v; pa.nq_t = d_nq_t; pa.nk_t = d_nk_t;
-    pa.cumf = g->d_cumf; pa.vidx = g->d_vidx; pa.tile_base = g->d_tile_base; pa.tile_win = g->d_tile_win;
-    pa.vcs = g->d_vcs; pa.tcs = g->d_tcs;
-    pa.Qp = base; pa.Kp = base + off_k; pa.Vp = base + off_v;
-    pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
-    pa.n_tiles = P.n_tiles; pa.eps = eps;
-    HIPCK(ctx, launch_pack(dtype, pa, s));
-    HIPCK(ctx, timing_mark(ctx, s));
-
-    SdpaArgs sa{};
-    sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
-    sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
-    sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
-    sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
-    sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
-    sa.scale_log2e = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
-    HIPCK(ctx, launch_sdpa(dtype, sa, s));
-    HIPCK(ctx, timing_mark(ctx, s));
-
-    HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
-    HIPCK(ctx, timing_mark(ctx, s));
-    return AWA_OK;
+    return forward_impl(ctx, g, dtype, d_vqkv, d_tqkv, d_nq_v, d_nk_v, d_nq_t, d_nk_t, eps, d_vattn,
+                        d_tattn, reinterpret_cast<hipStream_t>(stream));
 }
 
 int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv, const float* h_tqkv,

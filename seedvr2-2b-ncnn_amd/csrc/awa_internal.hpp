@@ -93,7 +93,13 @@ struct awa_ctx {
     // bracketing pack, attention and text average on the call's stream.
     bool timing = false;
     std::vector<hipEvent_t> ev_free;
-    std::vector<hipEvent_t> ev_used;
+    std::vector<hipEvent_t> ev_used;      // awa_forward: 4 per call
+    std::vector<hipEvent_t> dit_ev_used;  // dit_layer_forward: 7 per layer
+    // DiT block workspace (activations between the projections) and a small
+    // buffer for the timestep MLP.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    float* small = nullptr;
 };
 
 struct awa_geom {
@@ -113,6 +119,22 @@ struct awa_geom {
 };
 
 namespace awa {
+
+// Host helpers shared by the C ABI translation units (awa_capi.cpp).
+void set_err(awa_ctx* ctx, const char* fmt, ...);
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev);
+    ~DeviceGuard();
+};
+// Grows a device buffer (freeing the old one, which waits for its users).
+hipError_t ensure_buffer(void** buf, size_t* have, size_t need);
+hipError_t event_mark(awa_ctx* ctx, std::vector<hipEvent_t>& list, hipStream_t s);
+// awa_forward without argument checks (shared with the block).
+int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
+                 const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
+                 float eps, void* d_vattn, void* d_tattn, hipStream_t s);
 
 // Kernel launchers (defined in the .hip files).
 hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s);

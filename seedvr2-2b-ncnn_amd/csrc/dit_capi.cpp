@@ -1,0 +1,251 @@
+// dit_capi.cpp — C ABI of the DiT block: one layer of DitVk::forward_latent
+// (dit_vk.cpp:517-632) as norm -> GEMM -> AWA -> GEMM -> norm -> GEMM -> GEMM
+// on the caller's stream.
+#include <cmath>
+#include <cstring>
+
+#include "dit_internal.hpp"
+
+using namespace awa;
+
+namespace {
+
+#define HIPCK(ctx, expr)                                                                     \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) {                                                              \
+            set_err(ctx, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,    \
+                    __LINE__);                                                               \
+            return AWA_EHIP;                                                                 \
+        }                                                                                    \
+    } while (0)
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool branch_ok(const dit_branch* b) {
+    return b && b->qkv_w && b->out_w && b->out_b && b->mlp_w && b->mlp_out_w && b->nq && b->nk &&
+           b->attn_shift && b->attn_scale && b->attn_gate && b->mlp_shift && b->mlp_scale && b->mlp_gate;
+}
+
+GemmProblem problem(const uint16_t* A, int lda, const uint16_t* W, int ldw, int M, int N, int K,
+                    void* C, int ldc) {
+    GemmProblem p{};
+    p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.M = M; p.N = N; p.K = K; p.C = C; p.ldc = ldc;
+    p.split = M;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dit_pack_mlp_weights(awa_ctx* ctx, const uint16_t* d_w_in, const uint16_t* d_w_gate, int mlp,
+                         uint16_t* d_w_cat, awa_stream_t stream) {
+    if (!ctx || !d_w_in || !d_w_gate || !d_w_cat || mlp <= 0 || mlp % 128 != 0) {
+        set_err(ctx, "dit_pack_mlp_weights: bad argument (mlp=%d must be a positive multiple of 128)", mlp);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    HIPCK(ctx, launch_pack_mlp(d_w_in, d_w_gate, mlp, d_w_cat, reinterpret_cast<hipStream_t>(stream)));
+    return AWA_OK;
+}
+
+int dit_time_embedding(awa_ctx* ctx, float t, const float* d_w_in, const float* d_b_in,
+                       const float* d_w_hid, const float* d_b_hid, const float* d_w_out,
+                       const float* d_b_out, float* d_emb, awa_stream_t stream) {
+    if (!ctx || !d_w_in || !d_b_in || !d_w_hid || !d_b_hid || !d_w_out || !d_b_out || !d_emb) {
+        set_err(ctx, "dit_time_embedding: null argument");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (!ctx->small) HIPCK(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->small), 8192 * sizeof(float)));
+    float* e0 = ctx->small;          // [256]
+    float* e1 = e0 + 256;            // [2560]
+    float* e2 = e1 + DIM;            // [2560]
+    HIPCK(ctx, launch_sinusoid(t, e0, 256, s));
+    HIPCK(ctx, launch_gemv_f32(d_w_in, d_b_in, e0, e1, 256, DIM, 1, s));
+    HIPCK(ctx, launch_gemv_f32(d_w_hid, d_b_hid, e1, e2, DIM, DIM, 1, s));
+    HIPCK(ctx, launch_gemv_f32(d_w_out, d_b_out, e2, d_emb, DIM, DIT_EMB, 0, s));
+    return AWA_OK;
+}
+
+int dit_gemm_bf16(awa_ctx* ctx, const uint16_t* d_A, const uint16_t* d_W, uint16_t* d_C, int M, int N,
+                  int K, awa_stream_t stream) {
+    if (!ctx || !d_A || !d_W || !d_C || M < 1 || N < 256 || N % 256 || K < 64 || K % 64) {
+        set_err(ctx, "dit_gemm_bf16: bad argument M=%d N=%d K=%d (N %% 256 == 0, K %% 64 == 0)", M, N, K);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    GemmBatch b{};
+    b.nprob = 1;
+    b.p[0] = problem(d_A, K, d_W, K, M, N, K, d_C, N);
+    HIPCK(ctx, launch_gemm(EPI_STORE, b, reinterpret_cast<hipStream_t>(stream)));
+    return AWA_OK;
+}
+
+int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb, const dit_branch* tb,
+                      const float* d_emb, int mlp, int txt_vid_only, float eps, float* d_x, int Lv,
+                      int TXT, awa_stream_t stream) {
+    if (!ctx || !g || !d_emb || !d_x || !branch_ok(vb) || !branch_ok(tb)) {
+        set_err(ctx, "dit_layer_forward: null argument or incomplete branch");
+        return AWA_EARG;
+    }
+    if (Lv != g->plan.Lv || TXT != g->plan.txt_len) {
+        set_err(ctx, "dit_layer_forward: Lv=%d TXT=%d do not match the geometry (Lv=%d TXT=%d)", Lv,
+                TXT, g->plan.Lv, g->plan.txt_len);
+        return AWA_EARG;
+    }
+    if (mlp <= 0 || mlp % 128 != 0 || !(eps > 0.f)) {
+        set_err(ctx, "dit_layer_forward: mlp=%d must be a positive multiple of 128, eps > 0", mlp);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool dual = vb != tb;
+    const int M = Lv + TXT;
+    const int Mm = txt_vid_only ? Lv : M;  // rows that run the MLP
+
+    // workspace: ada [12][2560] f32 | h [M][2560] | qkv [M][7680] | attn [M][2560] | u [M][mlp]
+    const size_t o_h = align256(12 * DIM * 4);
+    const size_t o_qkv = o_h + align256((size_t)M * DIM * 2);
+    const size_t o_att = o_qkv + align256((size_t)M * QKV * 2);
+    const size_t o_u = o_att + align256((size_t)M * DIM * 2);
+    const size_t need = o_u + align256((size_t)M * mlp * 2);
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, need));
+    char* ws = static_cast<char*>(ctx->ws);
+    float* ada = reinterpret_cast<float*>(ws);
+    uint16_t* h = reinterpret_cast<uint16_t*>(ws + o_h);
+    uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + o_qkv);
+    uint16_t* att = reinterpret_cast<uint16_t*>(ws + o_att);
+    uint16_t* u = reinterpret_cast<uint16_t*>(ws + o_u);
+    auto V = [&](int f, int k) { return ada + (size_t)(f * 6 + k) * DIM; };  // a_sc a_sh a_g m_sc m_sh m_g
+    auto mark = [&]() { return event_mark(ctx, ctx->dit_ev_used, s); };
+
+    HIPCK(ctx, mark());
+    AdaArgs aa{};
+    aa.emb = d_emb;
+    aa.out = ada;
+    const dit_branch* br[2] = {vb, tb};
+    for (int f = 0; f < 2; f++) {
+        aa.vec[f][0] = br[f]->attn_scale; aa.vec[f][1] = br[f]->attn_shift; aa.vec[f][2] = br[f]->attn_gate;
+        aa.vec[f][3] = br[f]->mlp_scale;  aa.vec[f][4] = br[f]->mlp_shift;  aa.vec[f][5] = br[f]->mlp_gate;
+    }
+    HIPCK(ctx, launch_ada(aa, s));
+    // attention norm + ada (dit_vk.cpp:530-545); last layer: text rows unmodulated
+    NormArgs na{};
+    na.x = d_x; na.h = h; na.M = M; na.split = Lv; na.eps = eps;
+    na.scale0 = V(0, 0); na.shift0 = V(0, 1);
+    na.scale1 = txt_vid_only ? nullptr : V(1, 0);
+    na.shift1 = txt_vid_only ? nullptr : V(1, 1);
+    HIPCK(ctx, launch_norm_ada(na, s));
+    HIPCK(ctx, mark());
+
+    // qkv projections (dit_vk.cpp:321-322), no bias
+    GemmBatch b{};
+    if (!dual) {
+        b.nprob = 1;
+        b.p[0] = problem(h, DIM, vb->qkv_w, DIM, M, QKV, DIM, qkv, QKV);
+    } else {
+        b.nprob = 2;
+        b.p[0] = problem(h, DIM, vb->qkv_w, DIM, Lv, QKV, DIM, qkv, QKV);
+        b.p[1] = problem(h + (size_t)Lv * DIM, DIM, tb->qkv_w, DIM, TXT, QKV, DIM, qkv + (size_t)Lv * QKV, QKV);
+    }
+    HIPCK(ctx, launch_gemm(EPI_STORE, b, s));
+    HIPCK(ctx, mark());
+
+    // the AWA op, bf16 boundary (awa_layer.cpp:338-451)
+    int rc = forward_impl(ctx, g, AWA_BF16, qkv, qkv + (size_t)Lv * QKV, vb->nq, vb->nk, tb->nq, tb->nk, eps,
+                          att, att + (size_t)Lv * DIM, s);
+    if (rc != AWA_OK) return rc;
+    HIPCK(ctx, mark());
+
+    // out projection + bias, attention gate, residual (dit_vk.cpp:461-462, 558-575)
+    b = GemmBatch{};
+    if (!dual) {
+        b.nprob = 1;
+        b.p[0] = problem(att, DIM, vb->out_w, DIM, M, DIM, DIM, d_x, DIM);
+        b.p[0].bias = vb->out_b;
+        b.p[0].gate0 = V(0, 2);
+        b.p[0].gate1 = txt_vid_only ? nullptr : V(1, 2);
+        b.p[0].split = Lv;
+    } else {
+        b.nprob = 2;
+        b.p[0] = problem(att, DIM, vb->out_w, DIM, Lv, DIM, DIM, d_x, DIM);
+        b.p[0].bias = vb->out_b;
+        b.p[0].gate0 = V(0, 2);
+        b.p[1] = problem(att + (size_t)Lv * DIM, DIM, tb->out_w, DIM, TXT, DIM, DIM, d_x + (size_t)Lv * DIM, DIM);
+        b.p[1].bias = tb->out_b;
+        b.p[1].gate0 = txt_vid_only ? nullptr : V(1, 2);
+    }
+    HIPCK(ctx, launch_gemm(EPI_RESID, b, s));
+    HIPCK(ctx, mark());
+
+    // MLP norm + ada (dit_vk.cpp:577-597); last layer: text rows skip the MLP
+    na = NormArgs{};
+    na.x = d_x; na.h = h; na.M = Mm; na.split = Lv; na.eps = eps;
+    na.scale0 = V(0, 3); na.shift0 = V(0, 4);
+    na.scale1 = V(1, 3); na.shift1 = V(1, 4);
+    HIPCK(ctx, launch_norm_ada(na, s));
+    HIPCK(ctx, mark());
+
+    // SwiGLU (dit_vk.cpp:465-472): u = silu(h Wg^T) * (h Win^T), then out, gate, residual
+    b = GemmBatch{};
+    if (!dual || txt_vid_only) {
+        b.nprob = 1;
+        b.p[0] = problem(h, DIM, vb->mlp_w, DIM, dual ? Lv : Mm, 2 * mlp, DIM, u, mlp);
+    } else {
+        b.nprob = 2;
+        b.p[0] = problem(h, DIM, vb->mlp_w, DIM, Lv, 2 * mlp, DIM, u, mlp);
+        b.p[1] = problem(h + (size_t)Lv * DIM, DIM, tb->mlp_w, DIM, TXT, 2 * mlp, DIM, u + (size_t)Lv * mlp, mlp);
+    }
+    HIPCK(ctx, launch_gemm(EPI_SWIGLU, b, s));
+    b = GemmBatch{};
+    if (!dual || txt_vid_only) {
+        b.nprob = 1;
+        b.p[0] = problem(u, mlp, vb->mlp_out_w, mlp, dual ? Lv : Mm, DIM, mlp, d_x, DIM);
+        b.p[0].gate0 = V(0, 5);
+        b.p[0].gate1 = V(1, 5);
+        b.p[0].split = Lv;
+    } else {
+        b.nprob = 2;
+        b.p[0] = problem(u, mlp, vb->mlp_out_w, mlp, Lv, DIM, mlp, d_x, DIM);
+        b.p[0].gate0 = V(0, 5);
+        b.p[1] = problem(u + (size_t)Lv * mlp, mlp, tb->mlp_out_w, mlp, TXT, DIM, mlp, d_x + (size_t)Lv * DIM, DIM);
+        b.p[1].gate0 = V(1, 5);
+    }
+    HIPCK(ctx, launch_gemm(EPI_RESID, b, s));
+    HIPCK(ctx, mark());
+    return AWA_OK;
+}
+
+int dit_timing_read(awa_ctx* ctx, double* ms_gemm, double* ms_awa, double* ms_eltwise, int* layers) {
+    if (!ctx) return AWA_EARG;
+    DeviceGuard dg(ctx->device);
+    // per layer: e0 norm e1 qkv e2 awa e3 out e4 norm e5 mlp e6
+    double gemm = 0, awa_ms = 0, elt = 0;
+    const size_t n = ctx->dit_ev_used.size() / 7;
+    int rc = AWA_OK;
+    for (size_t i = 0; i < n && rc == AWA_OK; i++) {
+        hipEvent_t* e = &ctx->dit_ev_used[7 * i];
+        float d[6] = {0, 0, 0, 0, 0, 0};
+        hipError_t r = hipEventSynchronize(e[6]);
+        for (int k = 0; k < 6 && r == hipSuccess; k++) r = hipEventElapsedTime(&d[k], e[k], e[k + 1]);
+        if (r != hipSuccess) {
+            set_err(ctx, "dit_timing_read: %s", hipGetErrorString(r));
+            rc = AWA_EHIP;
+        }
+        elt += d[0] + d[4];
+        gemm += d[1] + d[3] + d[5];
+        awa_ms += d[2];
+    }
+    ctx->ev_free.insert(ctx->ev_free.end(), ctx->dit_ev_used.begin(), ctx->dit_ev_used.end());
+    ctx->dit_ev_used.clear();
+    if (ms_gemm) *ms_gemm = gemm;
+    if (ms_awa) *ms_awa = awa_ms;
+    if (ms_eltwise) *ms_eltwise = elt;
+    if (layers) *layers = (int)n;
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// dit_eltwise.hip — row-wise and small kernels of the DiT block.
+//
+//   norm_ada   RMSNorm (no affine, dit_vk.cpp:48-52) then the ada modulation
+//              x * scale + shift (dit_vk.cpp:532-545, 584-597), bf16 out:
+//              the A operand of the next projection.  One wave64 per row,
+//              HBM-bound (reads 10 KiB fp32, writes 5 KiB bf16 per row).
+//   ada        AdaCompose (ada_compose.cpp:165-235): emb[6d + K_MAP[k]] +
+//              branch vector, the 12 modulation vectors of a layer.
+//   pack_mlp   interleave proj_in / proj_in_gate rows for the fused SwiGLU.
+//   gemv_f32   the timestep MLP (M = 1 linears, dit_vk.cpp:303-309).
+#include <cmath>
+
+#include "dit_internal.hpp"
+
+namespace awa {
+
+namespace {
+
+__device__ inline uint32_t bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+constexpr int PER_LANE4 = DIM / 4 / 64;  // float4s per lane per 2560-wide row
+
+__global__ __launch_bounds__(256) void norm_ada_kernel(NormArgs a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= a.M) return;
+    const float4* x = reinterpret_cast<const float4*>(a.x + (size_t)row * DIM);
+    float4 v[PER_LANE4];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER_LANE4; i++) {
+        v[i] = x[i * 64 + lane];
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)DIM + a.eps);
+    const bool second = row >= a.split;
+    const float* sc = second ? a.scale1 : a.scale0;
+    const float* sh = second ? a.shift1 : a.shift0;
+    uint2* out = reinterpret_cast<uint2*>(a.h + (size_t)row * DIM);
+#pragma unroll
+    for (int i = 0; i < PER_LANE4; i++) {
+        const int c = (i * 64 + lane) * 4;
+        float o0 = v[i].x * r, o1 = v[i].y * r, o2 = v[i].z * r, o3 = v[i].w * r;
+        if (sc) {
+            const float4 s = *reinterpret_cast<const float4*>(sc + c);
+            const float4 t = *reinterpret_cast<const float4*>(sh + c);
+            o0 = o0 * s.x + t.x;
+            o1 = o1 * s.y + t.y;
+            o2 = o2 * s.z + t.z;
+            o3 = o3 * s.w + t.w;
+        }
+        out[i * 64 + lane] = make_uint2(bf16_rne(o0) | (bf16_rne(o1) << 16), bf16_rne(o2) | (bf16_rne(o3) << 16));
+    }
+}
+
+// K_MAP of ada_compose.cpp:16: a_sc->1, a_sh->0, a_g->2, m_sc->4, m_sh->3, m_g->5
+__constant__ int kAdaSlot[6] = {1, 0, 2, 4, 3, 5};
+
+__global__ __launch_bounds__(256) void ada_kernel(AdaArgs a) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= 12 * DIM) return;
+    const int d = i % DIM, k = (i / DIM) % 6, f = i / (6 * DIM);
+    a.out[i] = a.emb[d * 6 + kAdaSlot[k]] + a.vec[f][k][d];
+}
+
+__global__ __launch_bounds__(256) void pack_mlp_kernel(const uint16_t* __restrict__ w_in,
+                                                       const uint16_t* __restrict__ w_gate,
+                                                       uint16_t* __restrict__ w_cat) {
+    const int r = blockIdx.x;          // row of the fused weight
+    const int blk = r >> 5, within = r & 31;
+    const uint16_t* src = ((blk & 1) ? w_gate : w_in) + (size_t)((blk >> 1) * 32 + within) * DIM;
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    uint4* d4 = reinterpret_cast<uint4*>(w_cat + (size_t)r * DIM);
+    for (int c = threadIdx.x; c < DIM / 8; c += 256) d4[c] = s4[c];
+}
+
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ W,
+                                                       const float* __restrict__ b,
+                                                       const float* __restrict__ x,
+                                                       float* __restrict__ y, int in, int out,
+                                                       int silu) {
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (o >= out) return;
+    const float* w = W + (size_t)o * in;
+    float acc = 0.f;
+    for (int i = lane; i < in; i += 64) acc += w[i] * x[i];
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        float v = acc + (b ? b[o] : 0.f);
+        if (silu) v = v / (1.f + expf(-v));
+        y[o] = v;
+    }
+}
+
+struct Sinusoid {
+    float v[256];
+};
+
+__global__ void sinusoid_kernel(Sinusoid s, float* e, int dim) {
+    const int j = threadIdx.x;
+    if (j < dim) e[j] = s.v[j];
+}
+
+}  // namespace
+
+hipError_t launch_norm_ada(const NormArgs& a, hipStream_t s) {
+    if (a.M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(norm_ada_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_ada(const AdaArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(ada_kernel, dim3((12 * DIM + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_mlp(const uint16_t* w_in, const uint16_t* w_gate, int mlp, uint16_t* w_cat,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(pack_mlp_kernel, dim3(2 * mlp), dim3(256), 0, s, w_in, w_gate, w_cat);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f32(const float* W, const float* b, const float* x, float* y, int in, int out,
+                           int silu, hipStream_t s) {
+    hipLaunchKernelGGL(gemv_f32_kernel, dim3((out + 3) / 4), dim3(256), 0, s, W, b, x, y, in, out, silu);
+    return hipGetLastError();
+}
+
+hipError_t launch_sinusoid(float t, float* e, int dim, hipStream_t s) {
+    // The 256 sinusoid values are formed on the host with the reference's
+    // expression (dit_vk.cpp:295-302) and passed by value.
+    Sinusoid v{};
+    const int half = dim / 2;
+    for (int j = 0; j < dim && j < 256; j++) {
+        // float argument, double exp, rounded to float: as C's exp()
+        const float freq = (j < half) ? (float)::exp((double)(-logf(10000.f) * j / half))
+                                      : (float)::exp((double)(-logf(10000.f) * (j - half) / half));
+        v.v[j] = (j < half) ? sinf(t * freq) : cosf(t * freq);
+    }
+    hipLaunchKernelGGL(sinusoid_kernel, dim3(1), dim3(256), 0, s, v, e, dim);
+    return hipGetLastError();
+}
+
+}  // namespace awa

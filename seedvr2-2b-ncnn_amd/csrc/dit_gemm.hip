@@ -1,0 +1,222 @@
+// dit_gemm.hip — bf16 MFMA GEMMs of the DiT block with fused epilogues.
+//
+// D = A W^T with A [M][K] (activations, bf16) and W [N][K] (nn.Linear /
+// ncnn InnerProduct layout, bf16); both operands are K-contiguous.  The
+// kernel forms the transposed product per 32x32 block, D^T[n][m] =
+// sum_k W[n][k] A[m][k], with v_mfma_f32_32x32x16_bf16 so that each lane
+// ends with four consecutive output features of one activation row, which
+// the epilogues store as 8- or 16-byte pieces of row-major outputs.
+//
+// Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
+// 128x128 wave tiles (16 accumulators per wave).  Both operand tiles are
+// double buffered in LDS (2 x 64 KiB) with a 16-byte-chunk XOR swizzle
+// (chunk ^ (row & 7)) so that the eight rows read by consecutive lanes hit
+// distinct banks.  Tiles are walked in groups of four m-tiles and assigned
+// to XCDs in contiguous ranges, so the 32 workgroups resident on one XCD
+// share A and W k-slices through its L2.
+//
+// Epilogues (the elementwise tail of each projection in dit_vk.cpp:517-632):
+//   EPI_STORE     C = bf16(acc)                               (qkv)
+//   EPI_RESID     X += gate[n] * (acc + bias[n]), X fp32      (out proj, MLP out)
+//   EPI_SWIGLU    U = bf16(silu(g) * h), W rows interleaved   (proj_in + proj_in_gate)
+#include "dit_internal.hpp"
+
+namespace awa {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+typedef __attribute__((address_space(1))) void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+constexpr int BN = 256, BM = 256, BK = 64;
+constexpr int ROW_E = BK;                 // bf16 per LDS row (128 B, 8 chunks)
+constexpr int STAGE_E = (BN + BM) * ROW_E;
+
+__device__ inline uint32_t bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ inline int xcd_remap(int nblk) {
+    const int per = (nblk + 7) >> 3;
+    return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+}
+
+template <int EPI>
+__device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4], int n_base,
+                                int m_base, int lane) {
+    const int hb = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int m = m_base + 32 * j + col;
+        if (m >= p.M) continue;
+        if constexpr (EPI == EPI_SWIGLU) {
+            // blocks (0,1) and (2,3): (in, gate) of feature groups q and q+1
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int fbase = (n_base >> 1) + 32 * q;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    uint32_t packed[2];
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        float o[2];
+#pragma unroll
+                        for (int t = 0; t < 2; t++) {
+                            const float h = acc[2 * q][j][4 * g + e + t];
+                            const float gt = acc[2 * q + 1][j][4 * g + e + t];
+                            o[t] = gt / (1.f + __expf(-gt)) * h;
+                        }
+                        packed[e >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
+                    }
+                    const int f = fbase + 8 * g + 4 * hb;
+                    uint16_t* dst = reinterpret_cast<uint16_t*>(p.C) + (size_t)m * p.ldc + f;
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int n = n_base + 32 * i + 8 * g + 4 * hb;
+                    const float a0 = acc[i][j][4 * g], a1 = acc[i][j][4 * g + 1];
+                    const float a2 = acc[i][j][4 * g + 2], a3 = acc[i][j][4 * g + 3];
+                    if constexpr (EPI == EPI_STORE) {
+                        uint16_t* dst = reinterpret_cast<uint16_t*>(p.C) + (size_t)m * p.ldc + n;
+                        *reinterpret_cast<uint2*>(dst) =
+                            make_uint2(bf16_rne(a0) | (bf16_rne(a1) << 16), bf16_rne(a2) | (bf16_rne(a3) << 16));
+                    } else {  // EPI_RESID
+                        float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n);
+                        const float* gp = m < p.split ? p.gate0 : p.gate1;
+                        float4 gt = make_float4(1.f, 1.f, 1.f, 1.f);
+                        if (gp) gt = *reinterpret_cast<const float4*>(gp + n);
+                        float* dst = reinterpret_cast<float*>(p.C) + (size_t)m * p.ldc + n;
+                        float4 x = *reinterpret_cast<float4*>(dst);
+                        // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
+                        x.x = gt.x * (a0 + b.x) + x.x;
+                        x.y = gt.y * (a1 + b.y) + x.y;
+                        x.z = gt.z * (a2 + b.z) + x.z;
+                        x.w = gt.w * (a3 + b.w) + x.w;
+                        *reinterpret_cast<float4*>(dst) = x;
+                    }
+                }
+        }
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
+    __shared__ __align__(16) uint16_t lds[2 * STAGE_E];
+    const int lid = xcd_remap(b.total_tiles);
+    if (lid >= b.total_tiles) return;
+    const int pi = lid < b.tiles0 ? 0 : 1;
+    const GemmProblem& p = b.p[pi];
+    int local = lid - (pi ? b.tiles0 : 0);
+    // grouped order: four m-tiles per group, n advancing across the group
+    constexpr int GM = 4;
+    const int group = local / (GM * p.n_tiles);
+    const int first_m = group * GM;
+    const int gm = min(p.m_tiles - first_m, GM);
+    const int in_group = local % (GM * p.n_tiles);
+    const int mt = first_m + in_group % gm;
+    const int nt = in_group / gm;
+    const int n0 = nt * BN, m0 = mt * BM;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int hb = lane >> 5, r32 = lane & 31;
+
+    // Operand tiles go straight from global memory into LDS
+    // (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
+    // M0 + 16 i).  One wave instruction fills 1 KiB = 8 swizzled rows; lane l
+    // lands in row r0 + l/8, physical chunk l%8, so it fetches logical chunk
+    // (l%8) ^ (row & 7) of that row.  Each wave issues 8 per operand tile.
+    const int lrow = lane >> 3, lch = (lane & 7) ^ (lrow & 7);
+    const uint16_t* Wp = p.W + (size_t)n0 * p.ldw;
+    auto load = [&](int k0, int stage) {
+        uint16_t* ws = lds + stage * STAGE_E;
+        uint16_t* as = ws + BN * ROW_E;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int blk = wave * 8 + i;              // 1 KiB block of the tile
+            const int row = blk * 8 + lrow;
+            const uint16_t* wsrc = Wp + (size_t)row * p.ldw + k0 + lch * 8;
+            const int m = min(m0 + row, p.M - 1);
+            const uint16_t* asrc = p.A + (size_t)m * p.lda + k0 + lch * 8;
+            __builtin_amdgcn_global_load_lds((gptr_t)wsrc, (lptr_t)(ws + blk * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gptr_t)asrc, (lptr_t)(as + blk * 512), 16, 0, 0);
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = p.K / BK;
+    load(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int stage = kt & 1;
+        if (kt + 1 < nk) load((kt + 1) * BK, stage ^ 1);
+        const uint16_t* ws = lds + stage * STAGE_E;
+        const uint16_t* as = ws + BN * ROW_E;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int ch = 2 * s + hb;
+            bf16x8 wf[4], af[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = wn * 128 + 32 * i + r32;
+                wf[i] = *reinterpret_cast<const bf16x8*>(ws + row * ROW_E + ((ch ^ (row & 7)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int row = wm * 128 + 32 * j + r32;
+                af[j] = *reinterpret_cast<const bf16x8*>(as + row * ROW_E + ((ch ^ (row & 7)) << 3));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane);
+}
+
+}  // namespace
+
+hipError_t launch_gemm(int epi, GemmBatch& b, hipStream_t s) {
+    b.total_tiles = 0;
+    for (int i = 0; i < b.nprob; i++) {
+        GemmProblem& p = b.p[i];
+        p.n_tiles = p.N / BN;
+        p.m_tiles = (p.M + BM - 1) / BM;
+        if (i == 0) b.tiles0 = p.n_tiles * p.m_tiles;
+        b.total_tiles += p.n_tiles * p.m_tiles;
+    }
+    if (b.nprob == 1) b.p[1] = b.p[0];
+    if (b.total_tiles == 0) return hipSuccess;
+    const int grid = ((b.total_tiles + 7) >> 3) << 3;
+    switch (epi) {
+        case EPI_STORE: hipLaunchKernelGGL(gemm_kernel<EPI_STORE>, dim3(grid), dim3(256), 0, s, b); break;
+        case EPI_RESID: hipLaunchKernelGGL(gemm_kernel<EPI_RESID>, dim3(grid), dim3(256), 0, s, b); break;
+        case EPI_SWIGLU: hipLaunchKernelGGL(gemm_kernel<EPI_SWIGLU>, dim3(grid), dim3(256), 0, s, b); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace awa

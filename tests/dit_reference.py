@@ -1,0 +1,93 @@
+"""Reference for one DiT layer at the block's precision (test infrastructure).
+
+layer_emulation() restates DitVk::forward_latent's layer body
+(dit_vk.cpp:517-632, swiglu :465-472, awa_forward :312-463) with numpy fp32
+GEMMs and the oracle's attention.  With bf16=True it rounds to bf16 (nearest
+even) exactly where the MI355X block stores bf16: the projection inputs, the
+qkv and attention outputs (AwaLayer's bf16 boundary, awa_layer.cpp:338-451)
+and the SwiGLU product; weights are taken as the bf16 values they are stored
+as.  With bf16=False it is the fp32 layer, checked against the C oracle's
+orc_dit_layer (tests/test_dit_cpu.py).
+"""
+import numpy as np
+
+DIM = 2560
+
+
+def rmsnorm_rows(x, eps):
+    """dit_vk.cpp:48-52: double-accumulated mean square, float scale."""
+    ss = (x.astype(np.float64) ** 2).sum(axis=1) / x.shape[1]
+    r = (np.float32(1.0) / np.sqrt(ss.astype(np.float32) + np.float32(eps))).astype(np.float32)
+    return x * r[:, None]
+
+
+def ada_vectors(emb, br):
+    """AdaCompose slots (ada_compose.cpp:16): emb[6d + k] + branch vector."""
+    return {"a_sc": emb[1::6] + br["attn_scale"], "a_sh": emb[0::6] + br["attn_shift"],
+            "a_g": emb[2::6] + br["attn_gate"], "m_sc": emb[4::6] + br["mlp_scale"],
+            "m_sh": emb[3::6] + br["mlp_shift"], "m_g": emb[5::6] + br["mlp_gate"]}
+
+
+def silu(v):
+    return v / (np.float32(1.0) + np.exp(-v))
+
+
+def layer_emulation(O, x, emb, vb, tb, geom, Lv, TXT, last=False, eps=1e-5, bf16=True):
+    """One layer on x [Lv+TXT, 2560] fp32; branches are dicts of fp32 numpy arrays with
+    keys qkv_w, out_w, out_b, mlp_in_w, mlp_g_w, mlp_out_w, nq, nk and the six ada vectors."""
+    rnd = O.bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
+    x = np.array(x, np.float32, copy=True)
+    xv, xt = x[:Lv], x[Lv:]
+    av, at = ada_vectors(emb, vb), ada_vectors(emb, tb)
+    hv = rnd(rmsnorm_rows(xv, eps) * av["a_sc"] + av["a_sh"])
+    ht = rmsnorm_rows(xt, eps)
+    if not last:
+        ht = ht * at["a_sc"] + at["a_sh"]
+    ht = rnd(ht)
+    qv = rnd(hv @ vb["qkv_w"].T)
+    qt = rnd(ht @ tb["qkv_w"].T)
+    va, ta = O.awa_forward(qv, qt, geom, vb["nq"], vb["nk"], tb["nq"], tb["nk"], eps=eps)
+    va, ta = rnd(va), rnd(ta)
+    xv += av["a_g"] * (va @ vb["out_w"].T + vb["out_b"])
+    ot = ta @ tb["out_w"].T + tb["out_b"]
+    xt += ot if last else at["a_g"] * ot
+    hv = rnd(rmsnorm_rows(xv, eps) * av["m_sc"] + av["m_sh"])
+    uv = rnd(silu(hv @ vb["mlp_g_w"].T) * (hv @ vb["mlp_in_w"].T))
+    xv += av["m_g"] * (uv @ vb["mlp_out_w"].T)
+    if not last:
+        ht = rnd(rmsnorm_rows(xt, eps) * at["m_sc"] + at["m_sh"])
+        ut = rnd(silu(ht @ tb["mlp_g_w"].T) * (ht @ tb["mlp_in_w"].T))
+        xt += at["m_g"] * (ut @ tb["mlp_out_w"].T)
+    return x
+
+
+def random_branch(rng, mlp, O=None, scale=0.02):
+    """Weights ~ N(0, 0.02) (bf16-representable if O is given), gains 1 + N(0, 0.02)."""
+    r = (lambda a: O.bf16_round(a)) if O is not None else (lambda a: a)
+    f = lambda *s: (scale * rng.standard_normal(s)).astype(np.float32)
+    br = {"qkv_w": r(f(7680, DIM)), "out_w": r(f(DIM, DIM)), "out_b": f(DIM),
+          "mlp_in_w": r(f(mlp, DIM)), "mlp_g_w": r(f(mlp, DIM)), "mlp_out_w": r(f(DIM, mlp)),
+          "nq": (1 + f(128)).astype(np.float32), "nk": (1 + f(128)).astype(np.float32)}
+    for k in ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate"):
+        br[k] = f(DIM)
+    return br
+
+
+def random_emb(rng, O, scale=0.02):
+    """time_embedding(1000) through random N(0, scale) timestep-MLP weights."""
+    ws = [(scale * rng.standard_normal(s)).astype(np.float32)
+          for s in ((DIM, 256), (DIM,), (DIM, DIM), (DIM,), (6 * DIM, DIM), (6 * DIM,))]
+    return O.time_embedding(1000.0, *ws), ws
+
+
+def to_device(br, mlp, ctx, dev):
+    """Device tensors of a branch in the block's storage formats."""
+    import torch
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, torch.bfloat16)
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, torch.float32)
+    d = {"qkv_w": bf(br["qkv_w"]), "out_w": bf(br["out_w"]), "out_b": f32(br["out_b"]),
+         "mlp_out_w": bf(br["mlp_out_w"])}
+    d["mlp_w"] = ctx.pack_mlp(bf(br["mlp_in_w"]), bf(br["mlp_g_w"]))
+    for k in ("nq", "nk", "attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate"):
+        d[k] = f32(br[k])
+    return d

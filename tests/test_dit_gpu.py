@@ -1,0 +1,105 @@
+"""GPU parity of the DiT block (include/dit_capi.h) against the layer reference.
+
+Bars: the plain GEMM kernel within bf16 output rounding of an fp32 product;
+one layer's hidden-state output cos >= 0.9999 (bf16 bar of the op's
+specification), checked also on the layer's update x_out - x_in (a stricter
+view, since x_in dominates x_out).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import metrics
+from dit_reference import layer_emulation, random_branch, random_emb, to_device
+
+pytestmark = pytest.mark.gpu
+
+BF16_COS = 0.9999
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("shape", [(5440, 7680, 2560), (58, 7680, 2560), (5498, 2560, 6912),
+                                   (1, 256, 64), (300, 512, 128)])
+def test_gemm_bf16(ctx, shape):
+    import torch
+    M, N, K = shape
+    note(f"gemm M={M} N={N} K={K}")
+    g = torch.Generator(device="cpu").manual_seed(M + N + K)
+    A = torch.randn((M, K), generator=g).to("cuda", torch.bfloat16)
+    W = (0.05 * torch.randn((N, K), generator=g)).to("cuda", torch.bfloat16)
+    C = ctx.gemm(A, W)
+    ref = torch.mm(A.float(), W.float().t().contiguous())
+    torch.cuda.synchronize()
+    cos, rel, _ = metrics(C.float().cpu().numpy(), ref.cpu().numpy())
+    note(f"  cos={cos:.8f} rel={rel:.2e}")
+    assert cos >= 0.99999 and rel <= 1e-2
+
+
+def test_gemm_rejects_bad_shapes(ctx, awa):
+    import torch
+    A = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
+    W = torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(awa.AwaError):
+        ctx.gemm(A, W)
+
+
+def test_time_embedding(oracle, ctx):
+    import torch
+    rng = np.random.default_rng(30)
+    emb_ref, ws = random_emb(rng, oracle)
+    dws = [torch.from_numpy(w).cuda() for w in ws]
+    emb = ctx.time_embedding(1000.0, *dws)
+    torch.cuda.synchronize()
+    cos, rel, _ = metrics(emb.cpu().numpy(), emb_ref)
+    assert cos >= 0.999999 and rel <= 1e-5, (cos, rel)
+
+
+def run_layer(oracle, ctx, grid, nw, TXT, shifted, mlp, kind, seed):
+    import torch
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+    og = oracle.Geometry(*grid, nw, TXT, shifted)
+    emb, _ = random_emb(rng, oracle)
+    vb = random_branch(rng, mlp, oracle)
+    tb = vb if kind == "shared" else random_branch(rng, mlp, oracle)
+    x = rng.standard_normal((og.Lv + TXT, 2560)).astype(np.float32)
+    last = kind == "last"
+    ref = layer_emulation(oracle, x, emb, vb, tb, og, og.Lv, TXT, last=last, bf16=True)
+    geom = ctx.build_geometry(*grid, nw, TXT, shifted)
+    dvb = to_device(vb, mlp, ctx, dev)
+    dtb = dvb if tb is vb else to_device(tb, mlp, ctx, dev)
+    dx = torch.from_numpy(x).to(dev)
+    demb = torch.from_numpy(emb).to(dev)
+    ctx.layer(geom, dvb, dtb, demb, dx, og.Lv, TXT, mlp=mlp, txt_vid_only=last)
+    torch.cuda.synchronize()
+    out = dx.cpu().numpy()
+    return x, out, ref, og.Lv
+
+
+@pytest.mark.parametrize("kind", ["shared", "dual", "last"])
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_layer_small(oracle, ctx, kind, shifted):
+    note(f"layer small {kind} shifted={shifted}")
+    x, out, ref, Lv = run_layer(oracle, ctx, (1, 12, 20), (4, 3, 3), 9, shifted, 256, kind, 40 + shifted)
+    for sl in (slice(0, Lv), slice(Lv, None)):
+        cos, rel, _ = metrics(out[sl], ref[sl])
+        dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
+        note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
+        assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
+
+
+@pytest.mark.parametrize("kind", ["shared", "dual"])
+def test_layer_1080p(oracle, ctx, kind):
+    """One full-size layer (1x68x80 grid, TXT 58, MLP 6912), odd (shifted) geometry."""
+    note(f"layer 1080p {kind}")
+    x, out, ref, Lv = run_layer(oracle, ctx, (1, 68, 80), (4, 3, 3), 58, 1, 6912, kind, 50)
+    for sl in (slice(0, Lv), slice(Lv, None)):
+        cos, rel, _ = metrics(out[sl], ref[sl])
+        dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
+        note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
+        assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
