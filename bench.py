@@ -60,12 +60,82 @@ def cpu_baseline(vq_bf16_f32, tq_bf16_f32, gains):
             "cpu": cpu_model(), "nproc": os.cpu_count()}
 
 
+def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912):
+    """32-layer DiT step at 1080p: time embedding (t=1000) + 32 layers, layers
+    0-9 with separate video/text branches, 10-31 shared, even layers unshifted,
+    odd shifted; weights N(0, 0.02) bf16 resident in HBM (42 branches)."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    Lv = GRID[0] * GRID[1] * GRID[2]
+
+    def rnd(*shape, dtype=torch.bfloat16, scale=0.02):
+        return (scale * torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)).to(dtype)
+
+    def branch():
+        b = {"qkv_w": rnd(7680, 2560), "out_w": rnd(2560, 2560), "out_b": rnd(2560, dtype=torch.float32),
+             "mlp_out_w": rnd(2560, mlp)}
+        b["mlp_w"] = ctx.pack_mlp(rnd(mlp, 2560), rnd(mlp, 2560))
+        b["nq"] = 1 + rnd(128, dtype=torch.float32)
+        b["nk"] = 1 + rnd(128, dtype=torch.float32)
+        for k in ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate"):
+            b[k] = rnd(2560, dtype=torch.float32)
+        return b
+
+    layers = []
+    for i in range(32):
+        vb = branch()
+        layers.append((vb, branch() if i < 10 else vb))
+    temb = [rnd(2560, 256, dtype=torch.float32), rnd(2560, dtype=torch.float32),
+            rnd(2560, 2560, dtype=torch.float32), rnd(2560, dtype=torch.float32),
+            rnd(15360, 2560, dtype=torch.float32), rnd(15360, dtype=torch.float32)]
+    geoms = [ctx.build_geometry(*GRID, NUM_WINDOWS, TXT, sh) for sh in (0, 1)]
+    x0 = torch.randn((Lv + TXT, 2560), generator=gen, device=dev, dtype=torch.float32)
+    x = torch.empty_like(x0)
+
+    def one_step():
+        x.copy_(x0)
+        emb = ctx.time_embedding(1000.0, *temb)
+        for i, (vb, tb) in enumerate(layers):
+            ctx.layer(geoms[i % 2], vb, tb, emb, x, Lv, TXT, mlp=mlp, txt_vid_only=False)
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    ctx.timing(True)
+    ctx.dit_timing_read()
+    ctx.timing_read()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_gemm, ms_awa, ms_elt, nl = ctx.dit_timing_read()
+    ctx.timing_read()
+    ctx.timing(False)
+    assert bool(torch.isfinite(x).all()), "non-finite hidden state"
+    step_s = (t1 - t0) / steps
+    M = Lv + TXT
+    gemm_flops = 32 * 2 * M * 2560 * (7680 + 2560 + 3 * mlp)
+    for g in geoms:
+        g.close()
+    return {"value": round(step_s, 5), "unit": "s per 32-layer DiT step", "steps": steps,
+            "warmup": warmup, "mlp": mlp,
+            "txt_semantics": "text rows processed on every layer (merged-graph order)",
+            "per_step_ms": {"gemm": round(ms_gemm / steps, 3), "awa": round(ms_awa / steps, 3),
+                            "norm_ada_eltwise": round(ms_elt / steps, 3)},
+            "gemm_tflops": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12, 1),
+            "gemm_frac_of_bf16_peak": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "layers_timed": nl}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dit", action="store_true", help="skip the 32-layer DiT step")
+    ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (4 times) to calibrate the "
                          "FETCH_SIZE/WRITE_SIZE counters, then exit")
@@ -186,6 +256,8 @@ def main():
                             "frac": round(qk_bytes / pack_avg_s / 1e9 / PEAK_HBM_GBS, 4)},
         "per_variant": per_variant,
     }
+    if not args.no_dit:
+        out["dit_step"] = dit_step(ctx, awa_hip, torch, args.dit_steps, 1)
     if not args.no_cpu_baseline:
         vqf = vq.float().cpu().numpy()
         tqf = tq.float().cpu().numpy()

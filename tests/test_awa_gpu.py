@@ -266,3 +266,14 @@ def test_error_paths(oracle, ctx, awa):
     vf[0, 1] += 1.0  # channel pair no longer repeated
     with pytest.raises(awa.AwaError):
         ctx.set_geometry(o.vidx.astype(np.float32), o.cumf.astype(np.float32), vf, o.txt_freq, o.nwin, o.Lv, 5)
+
+
+def test_cpp_host_mirror():
+    """The C++ AwaLayer / AwaVk mirror (csrc/awa_layer.hpp) as a standalone
+    executable, like the reference's own test programs."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "bin", "test_awa_layer")
+    assert os.path.exists(exe), "build it: make -C seedvr2-2b-ncnn_amd tests"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
