@@ -236,6 +236,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     pa.Qp = base; pa.Kp = base + off_k; pa.Vp = base + off_v;
     pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
     pa.n_tiles = P.n_tiles; pa.eps = eps;
+    pa.qscale = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
     HIPCK(ctx, launch_pack(dtype, pa, s));
     HIPCK(ctx, timing_mark(ctx, s));
 
@@ -245,7 +246,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
     sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
-    sa.scale_log2e = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
+    sa.scale_log2e = 1.0f;  // the pack kernel folded the scale into Q
     HIPCK(ctx, launch_sdpa(dtype, sa, s));
     HIPCK(ctx, timing_mark(ctx, s));
 

@@ -9,6 +9,11 @@
 //   Kp[h][k][slot 0..63][d 0..127]   normalised + rotated keys
 //   Vp[h][k][d 0..127][slot 0..63]   values, transposed inside the tile
 // in the storage type of the op (bf16 or fp32).  Unused slots are zero.
+// Queries carry the softmax scale times log2(e), so scores come out in log2
+// units.  In bf16 storage the V^T slots of every 16-key group are stored in
+// the order 0-3, 8-11, 4-7, 12-15, which is the order in which the MFMA
+// accumulator of S^T hands the probabilities to the P.V product: a lane's
+// eight V^T values then sit in one 16-byte chunk.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -159,6 +164,7 @@ struct PackArgs {
     void* Vp;
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles;
     float eps;
+    float qscale;          // folded into Q: softmax scale 1/sqrt(128) times log2(e)
 };
 hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s);
 
@@ -173,7 +179,7 @@ struct SdpaArgs {
     void* vattn;
     float* tpart;          // [nwin][txt_len][2560] fp32 text partials
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles, n_items, nwin;
-    float scale_log2e;     // (1/sqrt(128)) * log2(e)
+    float scale_log2e;     // multiplier of the scores (1 when Q carries the scale)
 };
 hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s);
 

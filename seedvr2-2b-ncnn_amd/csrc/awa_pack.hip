@@ -162,6 +162,8 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
                 k[2 * p + 1] = k1 * cs.x + k0 * cs.y;
             }
         }
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] *= a.qscale;
         Io<T>::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
         Io<T>::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
         if constexpr (sizeof(T) == 2) {
@@ -190,7 +192,15 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
             T e[EPC];
         } tmp;
 #pragma unroll
-        for (int j = 0; j < EPC; j++) tmp.e[j] = vs[sc * EPC + j][d];
+        for (int j = 0; j < EPC; j++) {
+            int slot = sc * EPC + j;
+            if constexpr (sizeof(T) == 2) {
+                // swap quads 1 and 2 of each 16-slot group (see awa_internal.hpp)
+                const int qd = (slot >> 2) & 3;
+                if (qd == 1 || qd == 2) slot ^= 12;
+            }
+            tmp.e[j] = vs[slot][d];
+        }
         *reinterpret_cast<uint4*>(Vt + (size_t)d * TILE + sc * EPC) = tmp.u;
     }
 }

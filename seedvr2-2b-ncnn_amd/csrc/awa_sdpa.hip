@@ -137,13 +137,35 @@ __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, 
 }
 
 // ----------------------------------------------------------------- bf16
-constexpr int KP16 = 136;                 // LDS pitch of a K row (elements)
-constexpr int VP16 = 68;                  // LDS pitch of a V^T row (elements)
-constexpr int KS16 = TILE * KP16;
-constexpr int STAGE16 = KS16 + HEAD_D * VP16;
+// Four wave64 per workgroup, 32 queries each (two 64-row query tiles), and two
+// workgroups per CU so that each SIMD holds two waves: while one runs its
+// softmax on the VALU the other keeps the matrix core busy.  K and V^T
+// tiles are copied global -> LDS with global_load_lds_dwordx4 (lane i of a
+// wave writes 16 bytes at M0 + 16 i) into a double buffer whose 16-byte
+// chunks are XOR-swizzled per row (swz_k, swz_v): the 16 rows read by a
+// quarter-wave then fall in distinct banks.  Online softmax keeps a stale maximum
+// until a new tile's maximum exceeds it by more than 2^8 (the output is
+// divided by the matching sum at the end, so the result is unchanged).
+typedef __attribute__((address_space(1))) void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+constexpr int KT_E = TILE * HEAD_D;         // bf16 elements of a K (or V^T) tile
+constexpr int STAGE2 = 2 * KT_E;            // K tile then V^T tile
+constexpr float RESCALE_LOG2 = 8.f;
+
+// LDS has 64 four-byte banks: a 256-byte window.  A K row is 256 bytes (16
+// chunks), so chunk ^ (row & 15) gives 16 consecutive rows 16 distinct chunk
+// slots.  A V^T row is 128 bytes: rows 2r and 2r+1 share a window in its two
+// halves, so chunk ^ ((row >> 1) & 7) spreads 16 consecutive rows likewise.
+__device__ inline int swz_k(int row, int chunk) {
+    return row * HEAD_D + ((chunk ^ (row & 15)) << 3);
+}
+__device__ inline int swz_v(int row, int chunk) {
+    return row * TILE + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
 
 __global__ __launch_bounds__(256, 2) void sdpa_bf16_kernel(SdpaArgs a) {
-    __shared__ __align__(16) uint16_t lds[2 * STAGE16];
+    __shared__ __align__(16) uint16_t lds[2 * STAGE2];
     const int nblk = a.n_items * HEADS;
     const int lid = xcd_remap(nblk);
     if (lid >= nblk) return;
@@ -161,40 +183,35 @@ __global__ __launch_bounds__(256, 2) void sdpa_bf16_kernel(SdpaArgs a) {
     const bool active = kq >= 0;
     const int qslot = (wave & 1) * 32 + n;
 
-    const size_t head_off = (size_t)h * a.n_tiles * TILE * HEAD_D;
-    const uint16_t* Qh = reinterpret_cast<const uint16_t*>(a.Qp) + head_off;
+    const size_t head_off = (size_t)h * a.n_tiles * KT_E;
     const uint16_t* Kh = reinterpret_cast<const uint16_t*>(a.Kp) + head_off;
     const uint16_t* Vh = reinterpret_cast<const uint16_t*>(a.Vp) + head_off;
 
     // B operand of S^T = K Q^T, k-step s: Q[slot][16s + 8hb .. +8]
     bf16x8 qf[8];
     if (active) {
-        const uint16_t* qrow = Qh + ((size_t)wt.tile(kq) * TILE + qslot) * HEAD_D + 8 * hb;
+        const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.Qp) + head_off +
+                               (size_t)wt.tile(kq) * KT_E + qslot * HEAD_D + 8 * hb;
 #pragma unroll
         for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
     }
 
-    uint4 kreg[4], vreg[4];
-    auto load_tile = [&](int kk) {
-        const size_t t = (size_t)wt.tile(kk) * TILE * HEAD_D;
-        const uint4* ksrc = reinterpret_cast<const uint4*>(Kh + t);
-        const uint4* vsrc = reinterpret_cast<const uint4*>(Vh + t);
+    // DMA of one K tile and one V^T tile: each wave fills 4 + 4 KiB.
+    const int krow_l = lane >> 4, kch = lane & 15;  // K: 4 rows of 16 chunks per KiB
+    const int vrow_l = lane >> 3, vch = lane & 7;   // V^T: 8 rows of 8 chunks per KiB
+    auto load_tile = [&](int kk, int stage) {
+        const size_t t = (size_t)wt.tile(kk) * KT_E;
+        uint16_t* ks = lds + stage * STAGE2;
+        uint16_t* vs = ks + KT_E;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            kreg[i] = ksrc[tid + 256 * i];
-            vreg[i] = vsrc[tid + 256 * i];
-        }
-    };
-    auto store_tile = [&](int stage) {
-        uint16_t* ks = lds + stage * STAGE16;
-        uint16_t* vs = ks + KS16;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<uint4*>(ks + (c >> 4) * KP16 + (c & 15) * 8) = kreg[i];
-            uint16_t* vd = vs + (c >> 3) * VP16 + (c & 7) * 8;
-            *reinterpret_cast<uint2*>(vd) = make_uint2(vreg[i].x, vreg[i].y);
-            *reinterpret_cast<uint2*>(vd + 4) = make_uint2(vreg[i].z, vreg[i].w);
+            const int blk = wave * 4 + i;
+            const int kr = blk * 4 + krow_l;
+            const uint16_t* ksrc = Kh + t + kr * HEAD_D + ((kch ^ (kr & 15)) << 3);
+            __builtin_amdgcn_global_load_lds((gptr_t)ksrc, (lptr_t)(ks + blk * 512), 16, 0, 0);
+            const int vr = blk * 8 + vrow_l;
+            const uint16_t* vsrc = Vh + t + vr * TILE + ((vch ^ ((vr >> 1) & 7)) << 3);
+            __builtin_amdgcn_global_load_lds((gptr_t)vsrc, (lptr_t)(vs + blk * 512), 16, 0, 0);
         }
     };
 
@@ -203,35 +220,80 @@ __global__ __launch_bounds__(256, 2) void sdpa_bf16_kernel(SdpaArgs a) {
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) oacc[dt][r] = 0.f;
+    // Running maximum m (log2 units) enters the score accumulator as its
+    // initial value -m, so the MFMA yields s - m directly.
     float m_i = -INFINITY, l_i = 0.f;
+    f32x16 mbias;
+#pragma unroll
+    for (int r = 0; r < 16; r++) mbias[r] = 0.f;
+    bool first = true;
 
-    load_tile(0);
-    store_tile(0);
+    load_tile(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int kk = 0; kk < nk; kk++) {
         const int stage = kk & 1;
-        if (kk + 1 < nk) load_tile(kk + 1);
+        if (kk + 1 < nk) load_tile(kk + 1, stage ^ 1);
         if (active) {
-            const uint16_t* ks = lds + stage * STAGE16;
-            const uint16_t* vs = ks + KS16;
+            const uint16_t* ks = lds + stage * STAGE2;
+            const uint16_t* vs = ks + KT_E;
             f32x16 sacc[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + swz_k(32 * kt + n, hb));
+                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], mbias, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s = 1; s < 8; s++)
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++) {
+                    const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + swz_k(32 * kt + n, 2 * s + hb));
+                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[kt], 0, 0, 0);
+                }
+            const int kvalid = wt.nvalid(kk);
+            if (kvalid < TILE) {
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = 32 * kt + 8 * (r >> 2) + 4 * hb + (r & 3);
+                        if (key >= kvalid) sacc[kt][r] = -INFINITY;
+                    }
+            }
+            // tile maximum relative to m
+            float mt = fmaxf(sacc[0][0], sacc[1][0]);
+#pragma unroll
+            for (int r = 1; r < 16; r++) mt = fmaxf(mt, fmaxf(sacc[0][r], sacc[1][r]));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            if (__any(first || mt > RESCALE_LOG2)) {
+                // raise m by mt (first tile: m = tile maximum); rare after the first tiles
+                const float up = first ? mt : fmaxf(mt, 0.f);
+                const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-up);
+                m_i = first ? mt : m_i + up;
+                l_i *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) oacc[dt][r] *= alpha;
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) sacc[kt][r] -= up;
+#pragma unroll
+                for (int r = 0; r < 16; r++) mbias[r] = -m_i;
+                first = false;
+            }
+            float ps = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++) {
-                    const bf16x8 af =
-                        *reinterpret_cast<const bf16x8*>(ks + (32 * kt + n) * KP16 + 16 * s + 8 * hb);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[s], sacc[kt], 0, 0, 0);
+                for (int r = 0; r < 16; r++) {
+                    const float p = __builtin_amdgcn_exp2f(sacc[kt][r]);
+                    sacc[kt][r] = p;
+                    ps += p;
                 }
-            const float alpha = softmax_tile(sacc, wt.nvalid(kk), hb, a.scale_log2e, m_i, l_i);
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) oacc[dt][r] *= alpha;
+            l_i += ps;
+            // O^T += V^T P^T
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
@@ -241,15 +303,13 @@ __global__ __launch_bounds__(256, 2) void sdpa_bf16_kernel(SdpaArgs a) {
                     for (int i = 0; i < 8; i++) pb[i] = (__bf16)sacc[kt][8 * c2 + i];
 #pragma unroll
                     for (int dt = 0; dt < 4; dt++) {
-                        const uint16_t* vrow = vs + (32 * dt + n) * VP16 + 32 * kt + 16 * c2 + 4 * hb;
-                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
-                        const bf16x8 af = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pb, oacc[dt], 0, 0, 0);
+                        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(
+                            vs + swz_v(32 * dt + n, 4 * kt + 2 * c2 + hb));
+                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[dt], 0, 0, 0);
                     }
                 }
         }
-        if (kk + 1 < nk) store_tile(stage ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
     if (!active) return;

@@ -9,9 +9,10 @@
 //
 // Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
 // 128x128 wave tiles (16 accumulators per wave).  Both operand tiles are
-// double buffered in LDS (2 x 64 KiB) with a 16-byte-chunk XOR swizzle
-// (chunk ^ (row & 7)) so that the eight rows read by consecutive lanes hit
-// distinct banks.  Tiles are walked in groups of four m-tiles and assigned
+// double buffered in LDS (2 x 64 KiB) with a 16-byte-chunk XOR swizzle,
+// chunk ^ ((row >> 1) & 7): LDS has 64 four-byte banks, a 128-byte row fills
+// half of that window, so the 16 rows read by a quarter-wave land in 16
+// distinct 16-byte bank groups.  Tiles are walked in groups of four m-tiles and assigned
 // to XCDs in contiguous ranges, so the 32 workgroups resident on one XCD
 // share A and W k-slices through its L2.
 //
@@ -31,9 +32,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
-constexpr int BN = 256, BM = 256, BK = 64;
-constexpr int ROW_E = BK;                 // bf16 per LDS row (128 B, 8 chunks)
+constexpr int BN = 256, BM = 256, BK = 32;
+constexpr int NSTAGE = 4;                 // LDS ring: three K-steps of DMA in flight
+constexpr int ROW_E = BK;                 // bf16 per LDS row (64 B, 4 chunks)
 constexpr int STAGE_E = (BN + BM) * ROW_E;
+constexpr int DMA_PER_STAGE = 8;          // global_load_lds per wave per stage
+
+// LDS has 64 four-byte banks (a 256-byte window); a 64-byte row is a quarter
+// of it, so chunk ^ ((row >> 2) & 3) gives the 16 rows read by a quarter-wave
+// 16 distinct 16-byte bank groups.
+__device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 2) & 3)) << 3); }
 
 __device__ inline uint32_t bf16_rne(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -111,7 +119,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4],
 
 template <int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
-    __shared__ __align__(16) uint16_t lds[2 * STAGE_E];
+    __shared__ __align__(16) uint16_t lds[NSTAGE * STAGE_E];
     const int lid = xcd_remap(b.total_tiles);
     if (lid >= b.total_tiles) return;
     const int pi = lid < b.tiles0 ? 0 : 1;
@@ -133,23 +141,29 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
 
     // Operand tiles go straight from global memory into LDS
     // (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
-    // M0 + 16 i).  One wave instruction fills 1 KiB = 8 swizzled rows; lane l
-    // lands in row r0 + l/8, physical chunk l%8, so it fetches logical chunk
-    // (l%8) ^ (row & 7) of that row.  Each wave issues 8 per operand tile.
-    const int lrow = lane >> 3, lch = (lane & 7) ^ (lrow & 7);
+    // M0 + 16 i).  One wave instruction fills 1 KiB = 16 swizzled rows; lane l
+    // lands in row r0 + l/4, physical chunk l%4, so it fetches the logical
+    // chunk that the swizzle maps there.  Each wave issues 4 + 4 per stage.
+    const int lrow = lane >> 2;
     const uint16_t* Wp = p.W + (size_t)n0 * p.ldw;
-    auto load = [&](int k0, int stage) {
-        uint16_t* ws = lds + stage * STAGE_E;
-        uint16_t* as = ws + BN * ROW_E;
+    const uint16_t* wsrc[4];
+    const uint16_t* asrc[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int blk = wave * 8 + i;              // 1 KiB block of the tile
-            const int row = blk * 8 + lrow;
-            const uint16_t* wsrc = Wp + (size_t)row * p.ldw + k0 + lch * 8;
-            const int m = min(m0 + row, p.M - 1);
-            const uint16_t* asrc = p.A + (size_t)m * p.lda + k0 + lch * 8;
-            __builtin_amdgcn_global_load_lds((gptr_t)wsrc, (lptr_t)(ws + blk * 512), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gptr_t)asrc, (lptr_t)(as + blk * 512), 16, 0, 0);
+    for (int i = 0; i < 4; i++) {
+        const int row = (wave * 4 + i) * 16 + lrow;
+        const int lch = (lane & 3) ^ ((row >> 2) & 3);
+        wsrc[i] = Wp + (size_t)row * p.ldw + lch * 8;
+        asrc[i] = p.A + (size_t)min(m0 + row, p.M - 1) * p.lda + lch * 8;
+    }
+    auto load = [&](int kt) {
+        uint16_t* ws = lds + (kt % NSTAGE) * STAGE_E;
+        uint16_t* as = ws + BN * ROW_E;
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int blk = wave * 4 + i;
+            __builtin_amdgcn_global_load_lds((gptr_t)(wsrc[i] + k0), (lptr_t)(ws + blk * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gptr_t)(asrc[i] + k0), (lptr_t)(as + blk * 512), 16, 0, 0);
         }
     };
 
@@ -162,36 +176,52 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const int nk = p.K / BK;
-    load(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int stage = kt & 1;
-        if (kt + 1 < nk) load((kt + 1) * BK, stage ^ 1);
-        const uint16_t* ws = lds + stage * STAGE_E;
-        const uint16_t* as = ws + BN * ROW_E;
+    // prologue: stages 0..2 in flight, wait for stage 0
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int ch = 2 * s + hb;
-            bf16x8 wf[4], af[4];
+    for (int s0 = 0; s0 < NSTAGE - 1; s0++)
+        if (s0 < nk) load(s0);
+    if (nk >= 3) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (nk == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // A bare barrier: __syncthreads() would also drain the DMA prefetch.
+    __builtin_amdgcn_s_barrier();
+
+    int wrow[4], arow[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        wrow[i] = wn * 128 + 32 * i + r32;
+        arow[i] = wm * 128 + 32 * i + r32;
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        if (kt + NSTAGE - 1 < nk) load(kt + NSTAGE - 1);
+        const uint16_t* ws = lds + (kt % NSTAGE) * STAGE_E;
+        const uint16_t* as = ws + BN * ROW_E;
+        // two k16 steps; fragments of both are read before the MFMAs
+        bf16x8 wf[2][4], af[2][4];
+#pragma unroll
+        for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int row = wn * 128 + 32 * i + r32;
-                wf[i] = *reinterpret_cast<const bf16x8*>(ws + row * ROW_E + ((ch ^ (row & 7)) << 3));
+                wf[s][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 2 * s + hb));
+                af[s][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 2 * s + hb));
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int row = wm * 128 + 32 * j + r32;
-                af[j] = *reinterpret_cast<const bf16x8*>(as + row * ROW_E + ((ch ^ (row & 7)) << 3));
-            }
+        for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[s][i], af[s][j], acc[i][j], 0, 0, 0);
+        // schedule: the 16 fragment reads first, then the 32 MFMAs back to back
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+        // stage kt+1 must have landed; younger stages may still be in flight
+        const int ahead = min(nk - 1 - kt, NSTAGE - 1);  // stages issued after kt
+        // (this wave's LDS reads of stage kt are complete: the MFMAs consumed them)
+        if (ahead >= 3) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
+        else if (ahead == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
     }
     epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane);
 }
