@@ -362,8 +362,8 @@ int awa_geom_build(awa_ctx* ctx, int t, int h, int w, const int32_t num_windows[
     else if ((e = dalloc(&g->d_vidx, (size_t)P.sumf)) != hipSuccess) fail(e, "alloc");
     else if ((e = dalloc(&g->d_vfreq, (size_t)P.sumf * ROPE_ROT)) != hipSuccess) fail(e, "alloc");
     else if ((e = dalloc(&g->d_tfreq, (size_t)P.nwin * txt_len * ROPE_ROT)) != hipSuccess) fail(e, "alloc");
-    else if ((e = dalloc(&g->d_vcs, (size_t)P.sumf * NPAIR)) != hipSuccess) fail(e, "alloc");
-    else if ((e = dalloc(&g->d_tcs, (size_t)txt_len * NPAIR)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_vcs, (size_t)P.sumf * CS_STRIDE)) != hipSuccess) fail(e, "alloc");
+    else if ((e = dalloc(&g->d_tcs, (size_t)txt_len * CS_STRIDE)) != hipSuccess) fail(e, "alloc");
     else if ((e = launch_geom_build(p, g, s)) != hipSuccess) fail(e, "geometry kernel");
     if (rc == AWA_OK) rc = upload_plan(ctx, g, s);
     if (rc == AWA_OK) {
@@ -471,8 +471,8 @@ int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf, const f
     step(dalloc(&g->d_vidx, (size_t)sumf));
     step(dalloc(&g->d_vfreq, (size_t)sumf * ROPE_ROT));
     step(dalloc(&g->d_tfreq, trows * ROPE_ROT));
-    step(dalloc(&g->d_vcs, (size_t)sumf * NPAIR));
-    step(dalloc(&g->d_tcs, tcs_rows * NPAIR));
+    step(dalloc(&g->d_vcs, (size_t)sumf * CS_STRIDE));
+    step(dalloc(&g->d_tcs, tcs_rows * CS_STRIDE));
     if (rc == AWA_OK) {
         step(hipMemcpyAsync(g->d_slices, P.slices.data(), P.slices.size() * 4, hipMemcpyHostToDevice, s));
         step(hipMemcpyAsync(g->d_cumf, cumf.data(), cumf.size() * 4, hipMemcpyHostToDevice, s));

@@ -10,19 +10,27 @@ namespace awa {
 
 namespace {
 
-__device__ inline uint32_t bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
+constexpr int CO_BLOCK = 64;  // small blocks: the output is only TXT x 2560
 
 template <bool kBf16Out>
-__global__ __launch_bounds__(256) void coalesce_kernel(const float* __restrict__ tpart,
-                                                       void* __restrict__ out, int nwin, int n4) {
-    const int i = blockIdx.x * 256 + threadIdx.x;  // one float4 of [TXT*2560]
+__global__ __launch_bounds__(CO_BLOCK) void coalesce_kernel(const float* __restrict__ tpart,
+                                                            void* __restrict__ out, int nwin, int n4) {
+    const int i = blockIdx.x * CO_BLOCK + threadIdx.x;  // one float4 of [TXT*2560]
     if (i >= n4) return;
     const float4* src = reinterpret_cast<const float4*>(tpart) + i;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int w = 0; w < nwin; w++) {
+    // Eight windows' loads in flight at a time; the adds stay in window order.
+    int w = 0;
+    for (; w + 8 <= nwin; w += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = src[(size_t)(w + j) * n4];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
+        }
+    }
+    for (; w < nwin; w++) {
         const float4 v = src[(size_t)w * n4];
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
@@ -71,12 +79,12 @@ inline unsigned grid_for(int64_t n) {
 hipError_t launch_coalesce(int dtype, const float* tpart, void* tattn, int nwin, int txt_len,
                            hipStream_t s) {
     const int n4 = txt_len * DIM / 4;
-    const unsigned blocks = (unsigned)((n4 + 255) / 256);
+    const unsigned blocks = (unsigned)((n4 + CO_BLOCK - 1) / CO_BLOCK);
     if (blocks == 0) return hipSuccess;
     if (dtype == AWA_BF16)
-        hipLaunchKernelGGL(coalesce_kernel<true>, dim3(blocks), dim3(256), 0, s, tpart, tattn, nwin, n4);
+        hipLaunchKernelGGL(coalesce_kernel<true>, dim3(blocks), dim3(CO_BLOCK), 0, s, tpart, tattn, nwin, n4);
     else
-        hipLaunchKernelGGL(coalesce_kernel<false>, dim3(blocks), dim3(256), 0, s, tpart, tattn, nwin, n4);
+        hipLaunchKernelGGL(coalesce_kernel<false>, dim3(blocks), dim3(CO_BLOCK), 0, s, tpart, tattn, nwin, n4);
     return hipGetLastError();
 }
 

@@ -5,7 +5,8 @@
 // (src/awa_vk.cpp:73-88, src/awa_layer.cpp:110-141).  Integer work only,
 // except the RoPE angle tables: angle = float(double(pos) * base[j]) exactly
 // as awa_window.cpp:94-130 forms it, plus a (cos, sin) table per channel pair
-// that the pack kernel stages through LDS.
+// (64 pairs per row; pair 63 is the identity for the unrotated channels
+// 126-127) that the pack kernel reads.
 #include "awa_internal.hpp"
 
 namespace awa {
@@ -97,12 +98,13 @@ __global__ __launch_bounds__(256) void geom_build_kernel(GeomParams p, int32_t* 
         const int tt = p.txt_len + lt;  // time positions start after the text
         float* fr = vfreq + (size_t)g * ROPE_ROT;
         for (int k = 0; k < ROPE_ROT; k++) fr[k] = (float)angle_of(p, k, tt, lh, lw);
-        float2* cs = vcs + (size_t)g * NPAIR;
+        float2* cs = vcs + (size_t)g * CS_STRIDE;
         for (int q = 0; q < NPAIR; q++) {
             float sn, cn;
             sincosf((float)angle_of(p, 2 * q, tt, lh, lw), &sn, &cn);
             cs[q] = make_float2(cn, sn);
         }
+        cs[NPAIR] = make_float2(1.f, 0.f);  // channels 126, 127 pass through
     }
     // Text rows: 1-D position ii on every axis, same table in every window
     // (awa_window.cpp:120-130).
@@ -113,12 +115,13 @@ __global__ __launch_bounds__(256) void geom_build_kernel(GeomParams p, int32_t* 
         for (int k = 0; k < ROPE_ROT; k++) fr[k] = (float)((double)ii * p.base[(k % 42) >> 1]);
     }
     for (int r = gtid; r < p.txt_len; r += gstride) {
-        float2* cs = tcs + (size_t)r * NPAIR;
+        float2* cs = tcs + (size_t)r * CS_STRIDE;
         for (int q = 0; q < NPAIR; q++) {
             float sn, cn;
             sincosf((float)((double)r * p.base[(2 * q % 42) >> 1]), &sn, &cn);
             cs[q] = make_float2(cn, sn);
         }
+        cs[NPAIR] = make_float2(1.f, 0.f);
     }
 }
 
@@ -130,14 +133,14 @@ __global__ __launch_bounds__(256) void geom_tables_kernel(const float* __restric
                                                           float2* __restrict__ tcs) {
     const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
     const int gstride = gridDim.x * blockDim.x;
-    const long nv = (long)sumf * NPAIR, nt = (long)trows * NPAIR;
+    const long nv = (long)sumf * CS_STRIDE, nt = (long)trows * CS_STRIDE;
     for (long i = gtid; i < nv + nt; i += gstride) {
         const bool txt = i >= nv;
         const long j = txt ? i - nv : i;
-        const long row = j / NPAIR, q = j % NPAIR;
-        const float f = txt ? tfreq[row * ROPE_ROT + 2 * q] : vfreq[row * ROPE_ROT + 2 * q];
-        float sn, cn;
-        sincosf(f, &sn, &cn);
+        const long row = j / CS_STRIDE, q = j % CS_STRIDE;
+        float sn = 0.f, cn = 1.f;
+        if (q < NPAIR)
+            sincosf(txt ? tfreq[row * ROPE_ROT + 2 * q] : vfreq[row * ROPE_ROT + 2 * q], &sn, &cn);
         (txt ? tcs : vcs)[j] = make_float2(cn, sn);
     }
 }
@@ -156,7 +159,7 @@ hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s) {
 
 hipError_t launch_geom_tables(const float* vfreq, const float* tfreq, int sumf, int trows,
                               float2* vcs, float2* tcs, hipStream_t s) {
-    long n = (long)(sumf + trows) * NPAIR;
+    long n = (long)(sumf + trows) * CS_STRIDE;
     long blocks = (n + 255) / 256;
     if (blocks < 1) blocks = 1;
     if (blocks > 4096) blocks = 4096;

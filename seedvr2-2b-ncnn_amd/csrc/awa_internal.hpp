@@ -28,9 +28,26 @@ namespace awa {
 
 constexpr int HEADS = 20, HEAD_D = 128, DIM = 2560, QKV = 7680;
 constexpr int ROPE_ROT = 126, NPAIR = 63;
+constexpr int CS_STRIDE = 64;      // (cos, sin) pairs per row of the RoPE tables; pair 63 is (1, 0)
 constexpr int TILE = 64;           // rows per packed tile
 constexpr int MAX_AXIS = 256;      // slices per axis accepted by the geometry kernel
 constexpr int MAX_WIN = 4096;      // windows accepted by the geometry kernel
+
+// Block index -> work index such that the hardware's round-robin dispatch of
+// consecutive blocks over the 8 XCDs hands each XCD one contiguous range of
+// work indices (and so one L2 for the data neighbouring indices share).  The
+// grid must be a multiple of 8; indices >= nblk are idle.
+__device__ inline int xcd_remap(int nblk) {
+    const int per = (nblk + 7) >> 3;
+    return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+}
+inline unsigned xcd_grid(long nblk) { return (unsigned)(((nblk + 7) >> 3) << 3); }
+
+// fp32 -> bf16 bits, round to nearest even (cast_f32_bf16.comp:24)
+__device__ inline uint32_t bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
 
 // Integer restatement of awa_window.cpp:15-78 along one axis.  The reference
 // forms shifted bounds as int((i - 0.5) * wX) in double; for integer i and wX
@@ -119,8 +136,8 @@ struct awa_geom {
     int32_t* d_items = nullptr;
     float* d_vfreq = nullptr;
     float* d_tfreq = nullptr;
-    float2* d_vcs = nullptr;   // [sumf][63] (cos, sin) per channel pair
-    float2* d_tcs = nullptr;   // [txt_sets*txt_len][63]
+    float2* d_vcs = nullptr;   // [sumf][64] (cos, sin) per channel pair, pair 63 = (1, 0)
+    float2* d_tcs = nullptr;   // [txt_sets*txt_len][64]
 };
 
 namespace awa {

@@ -1,12 +1,16 @@
 // awa_pack.hip — fused qk RMSNorm + 3-D RoPE + window partition.
 //
-// One workgroup per (64-row tile, head).  It gathers the tile's rows from
-// vqkv / tqkv (window order through vidx, awa_vk.cpp:73-88), normalises q and k
-// per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 + eps), y = x / r * g),
-// rotates channel pairs (2i, 2i+1) for i < 63 (dit_vk.cpp:62-71) with the
-// (cos, sin) rows staged in LDS, and writes the packed tiles the SDPA kernel
-// reads: Qp/Kp row-major per tile, Vp transposed per tile (see
-// awa_internal.hpp).  HBM-bound: every input byte of q, k, v is read once.
+// One workgroup per (64-row tile, head); the 20 heads of a tile are
+// neighbouring work indices on one XCD, so the tile's (cos, sin) rows come
+// from HBM once and from that XCD's L2 for the other heads.  It gathers the
+// tile's rows from vqkv / tqkv (window order through vidx, awa_vk.cpp:73-88),
+// normalises q and k per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 +
+// eps), y = x / r * g), rotates channel pairs (2i, 2i+1) for i < 63
+// (dit_vk.cpp:62-71; pair 63 of the table is the identity) and writes the
+// packed tiles the SDPA kernel reads: Qp/Kp row-major per tile, Vp transposed
+// per tile (layout in awa_internal.hpp).  HBM-bound: every q, k, v byte is
+// read once and every packed byte written once; all loads of a thread are
+// issued before the first use.
 #include "awa_internal.hpp"
 
 namespace awa {
@@ -15,9 +19,11 @@ namespace {
 
 template <typename T> struct Io;
 
-template <> struct Io<uint16_t> {  // bf16 storage
-    static __device__ inline void load8(const uint16_t* p, float* x) {
-        const uint4 u = *reinterpret_cast<const uint4*>(p);
+template <> struct Io<uint16_t> {  // bf16 storage: 8 channels in one 16-byte load
+    using Raw = uint4;
+    static __device__ inline Raw load(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+    static __device__ inline Raw zero() { return make_uint4(0, 0, 0, 0); }
+    static __device__ inline void widen(const Raw& u, float* x) {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -25,27 +31,25 @@ template <> struct Io<uint16_t> {  // bf16 storage
             x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
         }
     }
-    static __device__ inline uint32_t rne(float f) {
-        // round to nearest even, cast_f32_bf16.comp:24
-        const uint32_t u = __float_as_uint(f);
-        return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-    }
     static __device__ inline void store8(uint16_t* p, const float* x) {
         uint4 u;
-        u.x = rne(x[0]) | (rne(x[1]) << 16);
-        u.y = rne(x[2]) | (rne(x[3]) << 16);
-        u.z = rne(x[4]) | (rne(x[5]) << 16);
-        u.w = rne(x[6]) | (rne(x[7]) << 16);
+        u.x = bf16_rne(x[0]) | (bf16_rne(x[1]) << 16);
+        u.y = bf16_rne(x[2]) | (bf16_rne(x[3]) << 16);
+        u.z = bf16_rne(x[4]) | (bf16_rne(x[5]) << 16);
+        u.w = bf16_rne(x[6]) | (bf16_rne(x[7]) << 16);
         *reinterpret_cast<uint4*>(p) = u;
     }
 };
 
 template <> struct Io<float> {
-    static __device__ inline void load8(const float* p, float* x) {
-        const float4 a = *reinterpret_cast<const float4*>(p);
-        const float4 b = *reinterpret_cast<const float4*>(p + 4);
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    struct Raw { float4 a, b; };
+    static __device__ inline Raw load(const float* p) {
+        return {*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+    }
+    static __device__ inline Raw zero() { return {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0)}; }
+    static __device__ inline void widen(const Raw& r, float* x) {
+        x[0] = r.a.x; x[1] = r.a.y; x[2] = r.a.z; x[3] = r.a.w;
+        x[4] = r.b.x; x[5] = r.b.y; x[6] = r.b.z; x[7] = r.b.w;
     }
     static __device__ inline void store8(float* p, const float* x) {
         *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
@@ -62,44 +66,75 @@ __device__ inline float row_sum16(float v) {
     return v;
 }
 
+// V staging tile in LDS, [slot][d] with a row pitch of VP 4-byte words.
+// bf16: VP = 65 (odd), so the 16-lane row writes (4-byte stores) of four rows
+// and the transposing column reads below both hit distinct banks;
+// fp32: VP = 129.
+template <typename T> struct VStage;
+template <> struct VStage<uint16_t> { static constexpr int VP = 65; };
+template <> struct VStage<float> { static constexpr int VP = 129; };
+
+constexpr int RPT = TILE / 16;  // rows per thread (16 rows per 256-thread pass)
+
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
-    constexpr int VROW = 128 + 16 / (int)sizeof(T);  // LDS pitch of the V staging tile
-    __shared__ __align__(16) T vs[TILE][VROW];
-    __shared__ float2 cs_s[TILE][NPAIR + 1];
+    using IO = Io<T>;
+    constexpr int VP = VStage<T>::VP;
+    __shared__ uint32_t vs[TILE * VP];
 
-    const int tile = blockIdx.x;
-    const int h = blockIdx.y;
+    const int nblk = a.n_tiles * HEADS;
+    const int lid = xcd_remap(nblk);
+    if (lid >= nblk) return;
+    const int tile = lid / HEADS;
+    const int h = lid - tile * HEADS;
     const int tid = threadIdx.x;
     const int c = tid & 15;     // 8-channel chunk of the head row
     const int r0 = tid >> 4;    // first slot handled by this thread
 
     const bool is_txt = tile >= a.n_vid_tiles;
-    int w = 0, set = 0, j0, nvalid;
+    int nvalid;
+    size_t cs_row0;             // table row of slot 0
+    const int32_t* vidx = nullptr;
+    const T* src;
     if (!is_txt) {
-        w = a.tile_win[tile];
-        j0 = (tile - a.tile_base[w]) * TILE;
-        nvalid = min(TILE, a.cumf[w + 1] - a.cumf[w] - j0);
+        const int w = a.tile_win[tile];
+        const int j0 = (tile - a.tile_base[w]) * TILE;
+        const int g0 = a.cumf[w] + j0;
+        nvalid = min(TILE, a.cumf[w + 1] - g0);
+        cs_row0 = g0;
+        vidx = a.vidx + g0;
+        src = reinterpret_cast<const T*>(a.vqkv);
     } else {
         const int tt = tile - a.n_vid_tiles;
-        set = tt / a.ntt;
-        j0 = (tt % a.ntt) * TILE;
+        const int set = tt / a.ntt;
+        const int j0 = (tt % a.ntt) * TILE;
         nvalid = min(TILE, a.txt_len - j0);
+        cs_row0 = (size_t)set * a.txt_len + j0;
+        src = reinterpret_cast<const T*>(a.tqkv) + (size_t)j0 * QKV;
     }
+    const float4* cst = reinterpret_cast<const float4*>(is_txt ? a.tcs : a.vcs);
     const float* gq = is_txt ? a.nq_t : a.nq_v;
     const float* gk = is_txt ? a.nk_t : a.nk_v;
+    const int col = h * HEAD_D + c * 8;
 
-    // Stage the (cos, sin) rows of the tile's slots in LDS; they are shared by
-    // q and k (and, across the grid, by all heads through L2).
-    for (int i = tid; i < TILE * NPAIR; i += 256) {
-        const int r = i / NPAIR, q = i % NPAIR;
-        float2 v = make_float2(1.f, 0.f);
-        if (r < nvalid) {
-            const size_t row = is_txt ? (size_t)set * a.txt_len + j0 + r
-                                      : (size_t)a.cumf[w] + j0 + r;
-            v = (is_txt ? a.tcs : a.vcs)[row * NPAIR + q];
+    // Issue every load of the thread: 4 rows x (q, k, v, 4 cos/sin pairs).
+    typename IO::Raw rq[RPT], rk[RPT], rv[RPT];
+    float4 cs[RPT][2];
+#pragma unroll
+    for (int kk = 0; kk < RPT; kk++) {
+        const int r = r0 + 16 * kk;
+        if (r < nvalid) {  // uniform across the 16 lanes of a row
+            const T* row = src + (size_t)(is_txt ? r : vidx[r]) * QKV + col;
+            rq[kk] = IO::load(row);
+            rk[kk] = IO::load(row + DIM);
+            rv[kk] = IO::load(row + 2 * DIM);
+            const float4* p = cst + ((cs_row0 + r) * CS_STRIDE + c * 4) / 2;
+            cs[kk][0] = p[0];
+            cs[kk][1] = p[1];
+        } else {
+            rq[kk] = rk[kk] = rv[kk] = IO::zero();
+            cs[kk][0] = cs[kk][1] = make_float4(1.f, 0.f, 1.f, 0.f);
         }
-        cs_s[r][q] = v;
     }
     float gqv[8], gkv[8];
 #pragma unroll
@@ -107,7 +142,6 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         gqv[i] = gq[c * 8 + i];
         gkv[i] = gk[c * 8 + i];
     }
-    __syncthreads();
 
     const size_t tile_off = ((size_t)h * a.n_tiles + tile) * TILE * HEAD_D;
     T* Qt = reinterpret_cast<T*>(a.Qp) + tile_off;
@@ -115,25 +149,12 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     T* Vt = reinterpret_cast<T*>(a.Vp) + tile_off;
 
 #pragma unroll
-    for (int kk = 0; kk < TILE / 16; kk++) {
+    for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
         float q[8], k[8], v[8];
-        if (r < nvalid) {  // uniform across the 16 lanes of a row
-            const T* row;
-            if (!is_txt) {
-                const int g = a.cumf[w] + j0 + r;
-                row = reinterpret_cast<const T*>(a.vqkv) + (size_t)a.vidx[g] * QKV;
-            } else {
-                row = reinterpret_cast<const T*>(a.tqkv) + (size_t)(j0 + r) * QKV;
-            }
-            const int col = h * HEAD_D + c * 8;
-            Io<T>::load8(row + col, q);
-            Io<T>::load8(row + DIM + col, k);
-            Io<T>::load8(row + 2 * DIM + col, v);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) q[i] = k[i] = v[i] = 0.f;
-        }
+        IO::widen(rq[kk], q);
+        IO::widen(rk[kk], k);
+        IO::widen(rv[kk], v);
         float sq = 0.f, sk = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -142,73 +163,77 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         }
         sq = row_sum16(sq);
         sk = row_sum16(sk);
-        const float rq = sqrtf(sq / (float)HEAD_D + a.eps);
-        const float rk = sqrtf(sk / (float)HEAD_D + a.eps);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            q[i] = q[i] / rq * gqv[i];
-            k[i] = k[i] / rk * gkv[i];
-        }
+        const float nq = sqrtf(sq / (float)HEAD_D + a.eps);
+        const float nk = sqrtf(sk / (float)HEAD_D + a.eps);
+        const float csv[8] = {cs[kk][0].x, cs[kk][0].y, cs[kk][0].z, cs[kk][0].w,
+                              cs[kk][1].x, cs[kk][1].y, cs[kk][1].z, cs[kk][1].w};
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const int P = c * 4 + p;  // channel pair index; pair 63 passes through
-            if (P < NPAIR) {
-                const float2 cs = cs_s[r][P];
-                const float q0 = q[2 * p], q1 = q[2 * p + 1];
-                q[2 * p] = q0 * cs.x - q1 * cs.y;
-                q[2 * p + 1] = q1 * cs.x + q0 * cs.y;
-                const float k0 = k[2 * p], k1 = k[2 * p + 1];
-                k[2 * p] = k0 * cs.x - k1 * cs.y;
-                k[2 * p + 1] = k1 * cs.x + k0 * cs.y;
-            }
+            const float cn = csv[2 * p], sn = csv[2 * p + 1];
+            const float q0 = q[2 * p] / nq * gqv[2 * p], q1 = q[2 * p + 1] / nq * gqv[2 * p + 1];
+            const float k0 = k[2 * p] / nk * gkv[2 * p], k1 = k[2 * p + 1] / nk * gkv[2 * p + 1];
+            q[2 * p] = (q0 * cn - q1 * sn) * a.qscale;
+            q[2 * p + 1] = (q1 * cn + q0 * sn) * a.qscale;
+            k[2 * p] = k0 * cn - k1 * sn;
+            k[2 * p + 1] = k1 * cn + k0 * sn;
         }
-#pragma unroll
-        for (int i = 0; i < 8; i++) q[i] *= a.qscale;
-        Io<T>::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
-        Io<T>::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
+        IO::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
+        IO::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
+        uint32_t* vrow = vs + r * VP;
         if constexpr (sizeof(T) == 2) {
-            uint4 u;
-            u.x = Io<uint16_t>::rne(v[0]) | (Io<uint16_t>::rne(v[1]) << 16);
-            u.y = Io<uint16_t>::rne(v[2]) | (Io<uint16_t>::rne(v[3]) << 16);
-            u.z = Io<uint16_t>::rne(v[4]) | (Io<uint16_t>::rne(v[5]) << 16);
-            u.w = Io<uint16_t>::rne(v[6]) | (Io<uint16_t>::rne(v[7]) << 16);
-            *reinterpret_cast<uint4*>(&vs[r][c * 8]) = u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) vrow[c * 4 + i] = bf16_rne(v[2 * i]) | (bf16_rne(v[2 * i + 1]) << 16);
         } else {
-            *reinterpret_cast<float4*>(&vs[r][c * 8]) = make_float4(v[0], v[1], v[2], v[3]);
-            *reinterpret_cast<float4*>(&vs[r][c * 8 + 4]) = make_float4(v[4], v[5], v[6], v[7]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) vrow[c * 8 + i] = __float_as_uint(v[i]);
         }
     }
     __syncthreads();
 
-    // Transposed V tile: Vt[d][slot]; lanes of a wave take 64 consecutive d
-    // (conflict-free LDS column reads), each wave one group of slots.
-    constexpr int EPC = 16 / (int)sizeof(T);        // elements per 16-byte chunk
-    constexpr int CPR = TILE / EPC;                 // chunks per V^T row
-    const int d = tid & 127;
+    // Transposed V tile Vt[d][slot], written as whole 128-byte (bf16) or
+    // 256-byte (fp32) rows by consecutive lanes.
+    if constexpr (sizeof(T) == 2) {
+        // Thread unit (d pair dp, 8-slot chunk sc): eight 4-byte LDS reads give
+        // the chunk for d = 2dp and d = 2dp + 1.  The slots of each 16-slot
+        // group go out in the order 0-3, 8-11, 4-7, 12-15.
 #pragma unroll
-    for (int sc = tid >> 7; sc < CPR; sc += 2) {
-        union {
-            uint4 u;
-            T e[EPC];
-        } tmp;
+        for (int it = 0; it < 2; it++) {
+            const int u = it * 256 + tid;
+            const int dp = u >> 3, sc = u & 7;
+            uint32_t lo[4], hi[4];
 #pragma unroll
-        for (int j = 0; j < EPC; j++) {
-            int slot = sc * EPC + j;
-            if constexpr (sizeof(T) == 2) {
-                // swap quads 1 and 2 of each 16-slot group (see awa_internal.hpp)
-                const int qd = (slot >> 2) & 3;
-                if (qd == 1 || qd == 2) slot ^= 12;
+            for (int j = 0; j < 8; j += 2) {
+                int s0 = sc * 8 + j;
+                const int qd = (s0 >> 2) & 3;
+                if (qd == 1 || qd == 2) s0 ^= 12;
+                const uint32_t w0 = vs[s0 * VP + dp], w1 = vs[(s0 + 1) * VP + dp];
+                lo[j >> 1] = (w0 & 0xffffu) | (w1 << 16);
+                hi[j >> 1] = (w0 >> 16) | (w1 & 0xffff0000u);
             }
-            tmp.e[j] = vs[slot][d];
+            uint16_t* dst = reinterpret_cast<uint16_t*>(Vt) + (size_t)(2 * dp) * TILE + sc * 8;
+            *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4*>(dst + TILE) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         }
-        *reinterpret_cast<uint4*>(Vt + (size_t)d * TILE + sc * EPC) = tmp.u;
+    } else {
+        // Thread unit (d, 4-slot chunk sc): 16 chunks per 64-slot row.
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int u = it * 256 + tid;
+            const int d = u >> 4, sc = u & 15;
+            float4 o;
+            o.x = __uint_as_float(vs[(sc * 4 + 0) * VP + d]);
+            o.y = __uint_as_float(vs[(sc * 4 + 1) * VP + d]);
+            o.z = __uint_as_float(vs[(sc * 4 + 2) * VP + d]);
+            o.w = __uint_as_float(vs[(sc * 4 + 3) * VP + d]);
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(Vt) + (size_t)d * TILE + sc * 4) = o;
+        }
     }
 }
 
 }  // namespace
 
 hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s) {
-    dim3 grid(a.n_tiles, HEADS), block(256);
+    const dim3 grid(xcd_grid((long)a.n_tiles * HEADS)), block(256);
     if (dtype == AWA_BF16)
         hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, block, 0, s, a);
     else

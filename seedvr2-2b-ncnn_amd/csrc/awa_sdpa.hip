@@ -55,15 +55,6 @@ __device__ inline WinTiles window_tiles(const SdpaArgs& a, int w) {
 // Hardware dispatches workgroup b to XCD b % 8.  Remap so that each XCD gets
 // a contiguous range of (head, item) ids: consecutive items of one head are
 // mostly the same window and share its K/V tiles through that XCD's L2.
-__device__ inline int xcd_remap(int nblk) {
-    const int per = (nblk + 7) >> 3;
-    return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-}
-
-__device__ inline uint32_t bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;  // cast_f32_bf16.comp:24
-}
 
 // Online-softmax update of one 64-key tile held as two 32x32 S^T accumulators
 // (lane: query column n = lane % 32; register r: key 8(r/4) + 4(lane/32) + r%4

@@ -7,14 +7,15 @@
 // ends with four consecutive output features of one activation row, which
 // the epilogues store as 8- or 16-byte pieces of row-major outputs.
 //
-// Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
-// 128x128 wave tiles (16 accumulators per wave).  Both operand tiles are
-// double buffered in LDS (2 x 64 KiB) with a 16-byte-chunk XOR swizzle,
-// chunk ^ ((row >> 1) & 7): LDS has 64 four-byte banks, a 128-byte row fills
-// half of that window, so the 16 rows read by a quarter-wave land in 16
-// distinct 16-byte bank groups.  Tiles are walked in groups of four m-tiles and assigned
-// to XCDs in contiguous ranges, so the 32 workgroups resident on one XCD
-// share A and W k-slices through its L2.
+// Workgroup tile 256 (n) x 256 (m), K step 32, four wave64 in a 2x2 grid of
+// 128x128 wave tiles (16 accumulators per wave).  Operand k-slices reach LDS
+// by direct global->LDS DMA (global_load_lds_dwordx4) into a 4-stage ring
+// (4 x 32 KiB), three stages in flight; the loop waits on the DMA counter
+// with explicit s_waitcnt and a bare s_barrier (a __syncthreads would drain
+// every outstanding load).  Rows are 64 bytes with a 16-byte-chunk XOR
+// swizzle, chunk ^ ((row >> 2) & 3).  Tiles are walked in groups of four
+// m-tiles and assigned to XCDs in contiguous ranges, so the workgroups
+// resident on one XCD share A and W k-slices through its L2.
 //
 // Epilogues (the elementwise tail of each projection in dit_vk.cpp:517-632):
 //   EPI_STORE     C = bf16(acc)                               (qkv)
@@ -36,22 +37,12 @@ constexpr int BN = 256, BM = 256, BK = 32;
 constexpr int NSTAGE = 4;                 // LDS ring: three K-steps of DMA in flight
 constexpr int ROW_E = BK;                 // bf16 per LDS row (64 B, 4 chunks)
 constexpr int STAGE_E = (BN + BM) * ROW_E;
-constexpr int DMA_PER_STAGE = 8;          // global_load_lds per wave per stage
 
 // LDS has 64 four-byte banks (a 256-byte window); a 64-byte row is a quarter
 // of it, so chunk ^ ((row >> 2) & 3) gives the 16 rows read by a quarter-wave
 // 16 distinct 16-byte bank groups.
 __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 2) & 3)) << 3); }
 
-__device__ inline uint32_t bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
-__device__ inline int xcd_remap(int nblk) {
-    const int per = (nblk + 7) >> 3;
-    return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-}
 
 template <int EPI>
 __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4], int n_base,
