@@ -4,6 +4,7 @@
 // items) with the same integer formulas the device kernel uses, owns the
 // device buffers, and enqueues pack -> SDPA -> coalesce on the caller's
 // stream without synchronising.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -87,7 +88,8 @@ hipError_t dalloc(T** p, size_t n) {
 
 void free_geom_buffers(awa_geom* g) {
     void* ptrs[] = {g->d_slices, g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win,
-                    g->d_items, g->d_vfreq, g->d_tfreq, g->d_vcs, g->d_tcs};
+                    g->d_items, g->d_sched_start, g->d_sched_desc, g->d_vfreq, g->d_tfreq,
+                    g->d_vcs, g->d_tcs};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -121,8 +123,77 @@ void plan_tiles(GeomPlan& P) {
     P.n_items = (int)P.items.size() / 4;
 }
 
+// Static longest-processing-time schedule of the persistent bf16 attention
+// kernel over n_slots resident workgroups.  A work item costs about its
+// window's key-tile count plus one tile for the prologue (Q load, first DMA).
+// All items of one (window, head) go to one XCD so that they share that
+// window's K/V tiles through the XCD's L2; groups are spread over the XCDs
+// longest first onto the least loaded XCD, then each XCD's items onto its
+// slots the same way.  Slot s is workgroup s, dispatched to XCD s % 8.
+void plan_schedule(GeomPlan& P, int n_slots) {
+    constexpr int XCDS = 8;
+    n_slots = std::max(XCDS, n_slots - n_slots % XCDS);
+    P.n_slots = n_slots;
+    const int per_xcd = n_slots / XCDS;
+    std::vector<int> win_cost(P.nwin);
+    for (int w = 0; w < P.nwin; w++) win_cost[w] = 10 * (P.tile_base[w + 1] - P.tile_base[w] + P.ntt) + 12;
+    struct Group { long cost; int h, w; };
+    std::vector<Group> groups;
+    std::vector<std::vector<int>> items_of(P.nwin);
+    for (int i = 0; i < P.n_items; i++) items_of[P.items[4 * i]].push_back(i);
+    for (int h = 0; h < HEADS; h++)
+        for (int w = 0; w < P.nwin; w++)
+            groups.push_back({(long)win_cost[w] * (long)items_of[w].size(), h, w});
+    std::stable_sort(groups.begin(), groups.end(), [](const Group& x, const Group& y) { return x.cost > y.cost; });
+    std::vector<long> xload(XCDS, 0);
+    std::vector<std::vector<int>> xwork(XCDS);  // work ids per XCD
+    for (const Group& gr : groups) {
+        const int x = (int)(std::min_element(xload.begin(), xload.end()) - xload.begin());
+        xload[x] += gr.cost;
+        for (int i : items_of[gr.w]) xwork[x].push_back(gr.h * P.n_items + i);
+    }
+    std::vector<std::vector<int>> slot_work(n_slots);
+    for (int x = 0; x < XCDS; x++) {
+        auto& wl = xwork[x];
+        std::stable_sort(wl.begin(), wl.end(), [&](int a, int b) {
+            return win_cost[P.items[4 * (a % P.n_items)]] > win_cost[P.items[4 * (b % P.n_items)]];
+        });
+        std::vector<long> sload(per_xcd, 0);
+        for (int id : wl) {
+            const int k = (int)(std::min_element(sload.begin(), sload.end()) - sload.begin());
+            sload[k] += win_cost[P.items[4 * (id % P.n_items)]];
+            slot_work[x + XCDS * k].push_back(id);
+        }
+    }
+    P.sched_start.assign(n_slots + 1, 0);
+    P.sched_desc.clear();
+    int n = 0;
+    for (int sl = 0; sl < n_slots; sl++) {
+        for (int id : slot_work[sl]) {
+            const int h = id / P.n_items, i = id % P.n_items, w = P.items[4 * i];
+            const int32_t d[8] = {h | (w << 8), P.items[4 * i + 1], P.items[4 * i + 2], P.cumf[w],
+                                  P.tile_base[w], P.tile_base[w + 1] - P.tile_base[w],
+                                  P.n_vid_tiles + (P.txt_sets == 1 ? 0 : w) * P.ntt,
+                                  P.cumf[w + 1] - P.cumf[w]};
+            P.sched_desc.insert(P.sched_desc.end(), d, d + 8);
+            n++;
+        }
+        P.sched_start[sl + 1] = n;
+    }
+}
+
 int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
-    const GeomPlan& P = g->plan;
+    GeomPlan& P = g->plan;
+    int n_cu = 0;
+    HIPCK(ctx, hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    plan_schedule(P, 2 * n_cu);
+    HIPCK(ctx, dalloc(&g->d_sched_start, P.sched_start.size()));
+    HIPCK(ctx, dalloc(&g->d_sched_desc, P.sched_desc.size()));
+    HIPCK(ctx, hipMemcpyAsync(g->d_sched_start, P.sched_start.data(), P.sched_start.size() * 4,
+                              hipMemcpyHostToDevice, s));
+    if (!P.sched_desc.empty())
+        HIPCK(ctx, hipMemcpyAsync(g->d_sched_desc, P.sched_desc.data(), P.sched_desc.size() * 4,
+                                  hipMemcpyHostToDevice, s));
     HIPCK(ctx, dalloc(&g->d_tile_base, P.tile_base.size()));
     HIPCK(ctx, dalloc(&g->d_tile_win, P.tile_win.size()));
     HIPCK(ctx, dalloc(&g->d_items, P.items.size()));
@@ -243,6 +314,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     SdpaArgs sa{};
     sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
     sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
+    sa.sched_start = g->d_sched_start; sa.sched_desc = g->d_sched_desc; sa.n_slots = P.n_slots;
     sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
     sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;

@@ -102,6 +102,15 @@ struct GeomPlan {
     std::vector<int32_t> tile_base;  // nwin+1, first video tile of window w
     std::vector<int32_t> tile_win;   // n_vid_tiles, window of each video tile
     std::vector<int32_t> items;      // n_items*4: window, first q tile, second q tile (-1), 0
+    // Persistent schedule of the bf16 attention kernel: one workgroup per
+    // resident slot (two per CU); slot s runs on XCD s % 8 and processes the
+    // work items sched_start[s] .. sched_start[s+1]) of sched_desc, longest
+    // first.  Each item is two int4: {head | window << 8, first query tile,
+    // second query tile (-1: none), cumf[window]}, {first video tile of the
+    // window, its video tile count, its first text tile, its token count}.
+    int n_slots = 0;
+    std::vector<int32_t> sched_start;  // n_slots+1
+    std::vector<int32_t> sched_desc;   // 8 per item, n_items*HEADS items
 };
 
 }  // namespace awa
@@ -134,6 +143,8 @@ struct awa_geom {
     int32_t* d_tile_base = nullptr;
     int32_t* d_tile_win = nullptr;
     int32_t* d_items = nullptr;
+    int32_t* d_sched_start = nullptr;
+    int32_t* d_sched_desc = nullptr;
     float* d_vfreq = nullptr;
     float* d_tfreq = nullptr;
     float2* d_vcs = nullptr;   // [sumf][64] (cos, sin) per channel pair, pair 63 = (1, 0)
@@ -193,6 +204,9 @@ struct SdpaArgs {
     const int32_t* cumf;
     const int32_t* vidx;
     const int32_t* tile_base;
+    const int32_t* sched_start;  // bf16 kernel: persistent schedule (GeomPlan)
+    const int32_t* sched_desc;
+    int n_slots;
     void* vattn;
     float* tpart;          // [nwin][txt_len][2560] fp32 text partials
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles, n_items, nwin;

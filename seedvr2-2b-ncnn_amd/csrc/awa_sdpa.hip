@@ -21,6 +21,8 @@
 // Video query rows are scattered back to token order (dit_vk.cpp:445-455);
 // text query rows go to per-window fp32 partials that the coalesce kernel
 // averages in window order (dit_vk.cpp:440-444).
+#include <type_traits>
+
 #include "awa_internal.hpp"
 
 namespace awa {
@@ -128,189 +130,478 @@ __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, 
 }
 
 // ----------------------------------------------------------------- bf16
-// Four wave64 per workgroup, 32 queries each (two 64-row query tiles), and two
-// workgroups per CU so that each SIMD holds two waves: while one runs its
-// softmax on the VALU the other keeps the matrix core busy.  K and V^T
-// tiles are copied global -> LDS with global_load_lds_dwordx4 (lane i of a
-// wave writes 16 bytes at M0 + 16 i) into a double buffer whose 16-byte
-// chunks are XOR-swizzled per row (swz_k, swz_v): the 16 rows read by a
-// quarter-wave then fall in distinct banks.  Online softmax keeps a stale maximum
-// until a new tile's maximum exceeds it by more than 2^8 (the output is
-// divided by the matching sum at the end, so the result is unchanged).
+// Persistent kernel: one workgroup of two wave64 per resident slot (two per
+// CU, one wave per SIMD), each processing the list of work items the host
+// planned for it (GeomPlan::sched_*): a work item is one head, one window and
+// one or two of its 64-row query tiles (one per wave).  A wave holds its query
+// tile as two 32-query column blocks (qb), so each K or V^T fragment read from
+// LDS feeds two MFMAs: with 32 queries per wave the fragment reads alone would
+// keep LDS (128 B/clk/CU) as busy as the matrix cores.  K and V^T tiles reach
+// LDS by DMA (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
+// M0 + 16 i), K in a ring of three tile slots and V^T in a ring of two (80 KiB
+// per workgroup).  While an item works on its last tile, the next item's
+// first two K tiles and first V^T tile go into the free slots and, after its
+// last unit, the next query tile is loaded, so an item starts without memory
+// round trips.
+//
+// The window's keys are processed in 32-key units u (two per tile).  With a
+// single wave per SIMD nothing hides latency but the wave's own instruction
+// stream, so each unit runs as two phases in which the matrix core and the
+// VALU work side by side:
+//
+//   A(u)  MFMA  S(u+1) = K(u+1) Q^T - m         (2 x 9 MFMAs: a bias k-step
+//                                               adds -m, m a bf16 value)
+//         VALU  P(u) = exp2(S(u))               (32 exponentials)
+//   B(u)  MFMA  O^T += V^T(u) P^T(u)            (16 MFMAs)
+//         VALU  row maximum of S(u+1), row sums of P(u)
+//
+// each MFMA and its share of VALU work issued by one asm statement so that
+// the compiler keeps them together.  The output accumulators O^T (128 AGPRs)
+// are pinned to the accumulation registers by the asm constraints; Q and the
+// scores live in VGPRs.  The running maximum m stays stale until a unit's
+// maximum exceeds it by more than 2^8 (the output is divided by the matching
+// sum at the end, so the result is unchanged); then O^T, the running sum and
+// the pending scores are rescaled.  The upper 32-key half of a short last tile
+// is fully masked (P = 0).
+//
+// Hazards the compiler cannot see through asm: every asm statement issues its
+// VALU work before its MFMA, which supplies the two wait states an MFMA needs
+// after a VALU write of its operands and keeps v_exp_f32 results from being
+// read by the next instruction (transcendental forwarding); explicit waits of
+// sixteen or more cover VALU reads of MFMA results (eleven are required after
+// an 8-pass MFMA).
 typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
 constexpr int KT_E = TILE * HEAD_D;         // bf16 elements of a K (or V^T) tile
-constexpr int STAGE2 = 2 * KT_E;            // K tile then V^T tile
 constexpr float RESCALE_LOG2 = 8.f;
 
-// LDS has 64 four-byte banks: a 256-byte window.  A K row is 256 bytes (16
-// chunks), so chunk ^ (row & 15) gives 16 consecutive rows 16 distinct chunk
-// slots.  A V^T row is 128 bytes: rows 2r and 2r+1 share a window in its two
-// halves, so chunk ^ ((row >> 1) & 7) spreads 16 consecutive rows likewise.
-__device__ inline int swz_k(int row, int chunk) {
-    return row * HEAD_D + ((chunk ^ (row & 15)) << 3);
+// Maximum and sum over lanes l and l ^ 32 (v_permlane32_swap: no LDS trip).
+__device__ inline float max_pair(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ inline int swz_v(int row, int chunk) {
-    return row * TILE + ((chunk ^ ((row >> 1) & 7)) << 3);
+__device__ inline float sum_pair(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__global__ __launch_bounds__(256, 2) void sdpa_bf16_kernel(SdpaArgs a) {
-    __shared__ __align__(16) uint16_t lds[2 * STAGE2];
-    const int nblk = a.n_items * HEADS;
-    const int lid = xcd_remap(nblk);
-    if (lid >= nblk) return;
-    const int h = lid / a.n_items;
-    const int item = lid % a.n_items;
-
-    const int4 it = reinterpret_cast<const int4*>(a.items)[item];
-    const int w = it.x;
-    const WinTiles wt = window_tiles(a, w);
-    const int nk = wt.nvt + wt.ntt;
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n = lane & 31, hb = lane >> 5;
-    const int kq = wave < 2 ? it.y : it.z;
-    const bool active = kq >= 0;
-    const int qslot = (wave & 1) * 32 + n;
-
-    const size_t head_off = (size_t)h * a.n_tiles * KT_E;
-    const uint16_t* Kh = reinterpret_cast<const uint16_t*>(a.Kp) + head_off;
-    const uint16_t* Vh = reinterpret_cast<const uint16_t*>(a.Vp) + head_off;
-
-    // B operand of S^T = K Q^T, k-step s: Q[slot][16s + 8hb .. +8]
-    bf16x8 qf[8];
-    if (active) {
-        const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.Qp) + head_off +
-                               (size_t)wt.tile(kq) * KT_E + qslot * HEAD_D + 8 * hb;
+// Phase A slot: x0, x1 = exp2(x0, x1) in place, then s += k q^T.  The VALU
+// instructions come first, so that they supply the two wait states an MFMA
+// needs after a VALU write of its operands, and nothing reads an exponential
+// in the instruction right after it.
+__device__ inline void exp_qk(f32x16& s, const bf16x8& k, const bf16x8& q, float& x0, float& x1) {
+    asm volatile(
+        "v_exp_f32 %1, %1\n\tv_exp_f32 %2, %2\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %3, %4, %0"
+        : "+v"(s), "+v"(x0), "+v"(x1)
+        : "v"(k), "v"(q));
+}
+// A slot without exponentials: s += k q^T.
+__device__ inline void qk_only(f32x16& s, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(k), "v"(q));
+}
+// First MFMA of a score chain: s = k q^T (accumulator from the constant 0).
+__device__ inline void exp_qk_first(f32x16& s, const bf16x8& k, const bf16x8& q, float& x0, float& x1) {
+    asm volatile(
+        "v_exp_f32 %1, %1\n\tv_exp_f32 %2, %2\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %3, %4, 0"
+        : "=&v"(s), "+v"(x0), "+v"(x1)
+        : "v"(k), "v"(q));
+}
+// Phase B slot: mx = max(mx, y0, y1), ps += x0 + x1, then o += v p^T.
+__device__ inline void max_sum_pv(f32x16& o, const bf16x8& v, const bf16x8& p, float& mx, float y0,
+                                  float y1, float& ps, float x0, float x1) {
+    asm volatile(
+        "v_max3_f32 %1, %1, %5, %6\n\tv_add_f32 %2, %2, %7\n\tv_add_f32 %2, %2, %8\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %3, %4, %0"
+        : "+a"(o), "+v"(mx), "+v"(ps)
+        : "v"(v), "v"(p), "v"(y0), "v"(y1), "v"(x0), "v"(x1));
+}
+// Phase B of an item's last unit (no next unit): ps += x0 + x1, o += v p^T.
+__device__ inline void sum_pv(f32x16& o, const bf16x8& v, const bf16x8& p, float& ps, float x0, float x1) {
+    asm volatile(
+        "v_add_f32 %1, %1, %4\n\tv_add_f32 %1, %1, %5\n\ts_nop 0\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %2, %3, %0"
+        : "+a"(o), "+v"(ps)
+        : "v"(v), "v"(p), "v"(x0), "v"(x1));
+}
+// bf16 value nearest to x (round to nearest even), as a float.
+__device__ inline float bf16_round(float x) { return __uint_as_float(bf16_rne(x) << 16); }
+// B-operand fragment of the bias k-step: element 0 of lanes 0-31 holds -m of
+// query column n (a bf16 value, so exact), everything else 0.  Paired with
+// the "ones" A fragment (key column 0 = 1), the MFMA adds -m to every score.
+__device__ inline bf16x8 bias_frag(float m, int hb) {
+    bf16x8 b;
 #pragma unroll
-        for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
+    for (int i = 0; i < 8; i++) b[i] = (__bf16)0.f;
+    if (hb == 0) b[0] = (__bf16)(-m);
+    return b;
+}
+
+// Waits after MFMA writes before anything else touches the results (ties the
+// registers so that nothing is scheduled across).
+__device__ inline void mfma_fence_v(f32x16 (&s)[2]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(s[0]), "+v"(s[1]));
+}
+__device__ inline void acc_fence(f32x16 (&o)[2][4]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                 : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]),
+                   "+a"(o[1][0]), "+a"(o[1][1]), "+a"(o[1][2]), "+a"(o[1][3]));
+}
+// acc *= alpha, register by register inside asm (the caller fences around).
+__device__ inline void acc_scale(f32x16& acc, float alpha) {
+#pragma unroll
+    for (int r = 0; r < 16; r += 4) {
+        float t;
+        asm volatile(
+            "v_accvgpr_read_b32 %4, %0\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %0, %4\n\t"
+            "v_accvgpr_read_b32 %4, %1\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %1, %4\n\t"
+            "v_accvgpr_read_b32 %4, %2\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %2, %4\n\t"
+            "v_accvgpr_read_b32 %4, %3\n\tv_mul_f32 %4, %4, %5\n\tv_accvgpr_write_b32 %3, %4"
+            : "+a"(acc[r]), "+a"(acc[r + 1]), "+a"(acc[r + 2]), "+a"(acc[r + 3]), "=&v"(t)
+            : "v"(alpha));
     }
-
-    // DMA of one K tile and one V^T tile: each wave fills 4 + 4 KiB.
-    const int krow_l = lane >> 4, kch = lane & 15;  // K: 4 rows of 16 chunks per KiB
-    const int vrow_l = lane >> 3, vch = lane & 7;   // V^T: 8 rows of 8 chunks per KiB
-    auto load_tile = [&](int kk, int stage) {
-        const size_t t = (size_t)wt.tile(kk) * KT_E;
-        uint16_t* ks = lds + stage * STAGE2;
-        uint16_t* vs = ks + KT_E;
+}
+// acc = 0 inside asm.
+__device__ inline void acc_zero(f32x16 (&o)[2][4]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int blk = wave * 4 + i;
-            const int kr = blk * 4 + krow_l;
-            const uint16_t* ksrc = Kh + t + kr * HEAD_D + ((kch ^ (kr & 15)) << 3);
-            __builtin_amdgcn_global_load_lds((gptr_t)ksrc, (lptr_t)(ks + blk * 512), 16, 0, 0);
-            const int vr = blk * 8 + vrow_l;
-            const uint16_t* vsrc = Vh + t + vr * TILE + ((vch ^ ((vr >> 1) & 7)) << 3);
-            __builtin_amdgcn_global_load_lds((gptr_t)vsrc, (lptr_t)(vs + blk * 512), 16, 0, 0);
+    for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 4)
+                asm volatile(
+                    "v_accvgpr_write_b32 %0, 0\n\tv_accvgpr_write_b32 %1, 0\n\t"
+                    "v_accvgpr_write_b32 %2, 0\n\tv_accvgpr_write_b32 %3, 0"
+                    : "=a"(o[qb][dt][r]), "=a"(o[qb][dt][r + 1]), "=a"(o[qb][dt][r + 2]),
+                      "=a"(o[qb][dt][r + 3]));
+}
+
+// Keys of a 32-key unit at or beyond kvalid get -inf.  Register r holds key
+// 8 (r / 4) + 4 hb + r % 4; groups of four registers valid for every lane are
+// skipped by a uniform test.
+__device__ inline void mask_unit(f32x16 (&s)[2], int kvalid, int hb) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        if (8 * g + 8 <= kvalid) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool ok = 8 * g + 4 * hb + j < kvalid;
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) s[qb][4 * g + j] = ok ? s[qb][4 * g + j] : -INFINITY;
         }
+    }
+}
+
+// A work item as planned on the host (two int4 per item, in slot order):
+// {h | w << 8, first query tile, second query tile (-1: none), cumf[w]},
+// {first video tile of w, video tiles of w, first text tile, f_w}.
+struct Work {
+    int h, w, q0, q1, g0, vbase, nvt, tbase, f;
+};
+__device__ inline Work load_work(const int4* d, int i) {
+    const int4 x = d[2 * i], y = d[2 * i + 1];
+    return Work{x.x & 255, x.x >> 8, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+}
+
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void sdpa_bf16_kernel(SdpaArgs a) {
+    __shared__ __align__(16) uint16_t lds[5 * KT_E];  // K ring (3 tile slots), V^T ring (2 slots)
+    const int wi0 = a.sched_start[blockIdx.x], wi1 = a.sched_start[blockIdx.x + 1];
+    if (wi0 >= wi1) return;
+    const int4* desc = reinterpret_cast<const int4*>(a.sched_desc);
+
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 31, hb = lane >> 5;
+    const size_t head_stride = (size_t)a.n_tiles * KT_E;
+
+    // DMA lane offsets.  K: instruction i of a wave fills the 1 KiB of rows
+    // 32 wave + 4 i .. +3; the lane at physical chunk lane % 16 of row
+    // 32 wave + 4 i + lane / 16 fetches logical chunk (lane % 16) ^ (row & 15).
+    // row & 15 = 4 (i & 3) + lane / 16, so instruction i + 4 is instruction i
+    // shifted by 16 rows.  V^T: instruction i fills rows 64 wave + 8 i .. +7,
+    // logical chunk (lane % 8) ^ ((row >> 1) & 7); instruction i + 2 is
+    // instruction i shifted by 16 rows.
+    int koff[4], voff[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = 32 * wave + 4 * i + (lane >> 4);
+        koff[i] = row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int row = 64 * wave + 8 * i + (lane >> 3);
+        voff[i] = row * TILE + (((lane & 7) ^ ((row >> 1) & 7)) << 3);
+    }
+    // tile index of key tile kk of work item W
+    auto tile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
+        return kk < W.nvt ? W.vbase + kk : W.tbase + (kk - W.nvt);
+    };
+    auto dma_k = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(a.Kp) + W.h * head_stride +
+                              (size_t)tile_of(W, kk) * KT_E;
+        uint16_t* dst = lds + slot * KT_E + wave * (KT_E / 2);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_global_load_lds((gptr_t)(src + (i >> 2) * 16 * HEAD_D + koff[i & 3]),
+                                            (lptr_t)(dst + i * 512), 16, 0, 0);
+    };
+    auto dma_v = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(a.Vp) + W.h * head_stride +
+                              (size_t)tile_of(W, kk) * KT_E;
+        uint16_t* dst = lds + (3 + slot) * KT_E + wave * (KT_E / 2);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_global_load_lds((gptr_t)(src + (i >> 1) * 16 * TILE + voff[i & 1]),
+                                            (lptr_t)(dst + i * 512), 16, 0, 0);
+    };
+    // The first K tiles and V^T tile of W into ring slots kb, kb + 1 and vb.
+    auto dma_first = [&](const Work& W, int kb, int vb) __attribute__((always_inline)) {
+        dma_k(W, 0, kb);
+        if (W.nvt + a.ntt > 1) dma_k(W, 1, (kb + 1) % 3);
+        dma_v(W, 0, vb);
+    };
+    // B operand of S^T = K Q^T for column block qb, k-step s:
+    // Q[slot 32 qb + n][16 s + 8 hb .. +8]
+    bf16x8 qf[2][8];
+    auto load_q = [&](const Work& W) __attribute__((always_inline)) {
+        const int kq = wave == 0 ? W.q0 : W.q1;
+        if (kq < 0) return;
+        const uint16_t* qt = reinterpret_cast<const uint16_t*>(a.Qp) + W.h * head_stride +
+                             (size_t)tile_of(W, kq) * KT_E + 8 * hb;
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                qf[qb][s] = *reinterpret_cast<const bf16x8*>(qt + (32 * qb + n) * HEAD_D + 16 * s);
     };
 
-    f32x16 oacc[4];
+    // LDS fragment addresses.  K fragment (k-step s) of a unit: row n of the
+    // unit, chunk 2 s + hb (rows 32 apart share the swizzle).  V^T fragment
+    // (unit half uh, c2, d-tile dt): row 32 dt + n, chunk 4 uh + 2 c2 + hb.
+    // The upper half (uh = 1) flips chunk bit 2, i.e. element-offset bit 5.
+    int kadr[8], vadr[2];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+    for (int s = 0; s < 8; s++) kadr[s] = n * HEAD_D + (((2 * s + hb) ^ (n & 15)) << 3);
 #pragma unroll
-        for (int r = 0; r < 16; r++) oacc[dt][r] = 0.f;
-    // Running maximum m (log2 units) enters the score accumulator as its
-    // initial value -m, so the MFMA yields s - m directly.
-    float m_i = -INFINITY, l_i = 0.f;
-    f32x16 mbias;
-#pragma unroll
-    for (int r = 0; r < 16; r++) mbias[r] = 0.f;
-    bool first = true;
+    for (int c = 0; c < 2; c++) vadr[c] = n * TILE + (((2 * c + hb) ^ ((n >> 1) & 7)) << 3);
 
-    load_tile(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kk = 0; kk < nk; kk++) {
-        const int stage = kk & 1;
-        if (kk + 1 < nk) load_tile(kk + 1, stage ^ 1);
-        if (active) {
-            const uint16_t* ks = lds + stage * STAGE2;
-            const uint16_t* vs = ks + KT_E;
-            f32x16 sacc[2];
+    // A fragment of the bias k-step: key column 0 (element 0 of lanes 0-31) = 1.
+    bf16x8 ones;
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + swz_k(32 * kt + n, hb));
-                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], mbias, 0, 0, 0);
-            }
-#pragma unroll
-            for (int s = 1; s < 8; s++)
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++) {
-                    const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + swz_k(32 * kt + n, 2 * s + hb));
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[kt], 0, 0, 0);
-                }
-            const int kvalid = wt.nvalid(kk);
-            if (kvalid < TILE) {
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int key = 32 * kt + 8 * (r >> 2) + 4 * hb + (r & 3);
-                        if (key >= kvalid) sacc[kt][r] = -INFINITY;
-                    }
-            }
-            // tile maximum relative to m
-            float mt = fmaxf(sacc[0][0], sacc[1][0]);
-#pragma unroll
-            for (int r = 1; r < 16; r++) mt = fmaxf(mt, fmaxf(sacc[0][r], sacc[1][r]));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            if (__any(first || mt > RESCALE_LOG2)) {
-                // raise m by mt (first tile: m = tile maximum); rare after the first tiles
-                const float up = first ? mt : fmaxf(mt, 0.f);
-                const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-up);
-                m_i = first ? mt : m_i + up;
-                l_i *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) oacc[dt][r] *= alpha;
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) sacc[kt][r] -= up;
-#pragma unroll
-                for (int r = 0; r < 16; r++) mbias[r] = -m_i;
-                first = false;
-            }
-            float ps = 0.f;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float p = __builtin_amdgcn_exp2f(sacc[kt][r]);
-                    sacc[kt][r] = p;
-                    ps += p;
-                }
-            l_i += ps;
-            // O^T += V^T P^T
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int c2 = 0; c2 < 2; c2++) {
-                    bf16x8 pb;
-#pragma unroll
-                    for (int i = 0; i < 8; i++) pb[i] = (__bf16)sacc[kt][8 * c2 + i];
-#pragma unroll
-                    for (int dt = 0; dt < 4; dt++) {
-                        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(
-                            vs + swz_v(32 * dt + n, 4 * kt + 2 * c2 + hb));
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[dt], 0, 0, 0);
-                    }
-                }
-        }
+    for (int i = 0; i < 8; i++) ones[i] = (__bf16)0.f;
+    if (hb == 0) ones[0] = (__bf16)1.f;
+
+    Work cur = load_work(desc, wi0);
+    int kb = 0, vb = 0;  // ring slots of the current item's key tile 0
+    dma_first(cur, kb, vb);
+    load_q(cur);
+
+    for (int wi = wi0; wi < wi1; wi++) {
+        const bool has_next = wi + 1 < wi1;
+        const Work nxt = load_work(desc, has_next ? wi + 1 : wi);
+        const int nk = cur.nvt + a.ntt;
+        const int kq = wave == 0 ? cur.q0 : cur.q1;
+        const bool active = kq >= 0;
+        auto nvalid = [&](int kk) __attribute__((always_inline)) {
+            return kk < cur.nvt ? min(TILE, cur.f - TILE * kk) : min(TILE, a.txt_len - TILE * (kk - cur.nvt));
+        };
+        auto k_ofs = [&](int u) __attribute__((always_inline)) {  // K rows of unit u
+            return ((kb + (u >> 1)) % 3) * KT_E + (u & 1) * 32 * HEAD_D;
+        };
+        auto unit_kv = [&](int u) __attribute__((always_inline)) {  // valid keys, <= 0: none
+            return nvalid(u >> 1) - 32 * (u & 1);
+        };
+
+        f32x16 oacc[2][4];
+        float scur[2][16];  // scores of the current unit relative to m (later exponentials)
+        bf16x8 bfr[2];      // bias fragments (-m)
+        float m_i[2] = {0.f, 0.f}, l_i[2] = {0.f, 0.f}, mtc[2] = {0.f, 0.f};
+        acc_zero(oacc);
+
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+
+        // Unit 0: raw scores, m = their row maximum (rounded to bf16), scores
+        // relative to m.
+        if (active) {
+            f32x16 s0[2];
+            bf16x8 kf[8];
+            const int ko = k_ofs(0);
+#pragma unroll
+            for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                f32x16 z;
+#pragma unroll
+                for (int r = 0; r < 16; r++) z[r] = 0.f;
+                s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[qb][0], z, 0, 0, 0);
+#pragma unroll
+                for (int st = 1; st < 8; st++)
+                    s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[qb][st], s0[qb], 0, 0, 0);
+            }
+            const int kv0 = unit_kv(0);
+            if (kv0 < 32) mask_unit(s0, kv0, hb);
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                float mx = fmaxf(s0[qb][0], s0[qb][1]);
+#pragma unroll
+                for (int r = 2; r < 16; r++) mx = fmaxf(mx, s0[qb][r]);
+                m_i[qb] = bf16_round(max_pair(mx));  // finite: unit 0 has a valid key
+                bfr[qb] = bias_frag(m_i[qb], hb);
+#pragma unroll
+                for (int r = 0; r < 16; r++) scur[qb][r] = s0[qb][r] - m_i[qb];
+            }
+        }
+
+        // One unit: phases A and B as described above.
+        auto unit = [&](int u, bool has_succ) __attribute__((always_inline)) {
+            // ---- stale-maximum rule for this unit's scores (mtc: their row max relative to m)
+            if (__any(mtc[0] > RESCALE_LOG2 || mtc[1] > RESCALE_LOG2)) {
+                float alpha[2];
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++) {
+                    // new m: a bf16 value at or above the unit maximum
+                    const float mn = mtc[qb] > 0.f ? bf16_round(m_i[qb] + mtc[qb]) : m_i[qb];
+                    const float up = mn - m_i[qb];
+                    alpha[qb] = __builtin_amdgcn_exp2f(-up);
+                    m_i[qb] = mn;
+                    bfr[qb] = bias_frag(mn, hb);
+                    l_i[qb] *= alpha[qb];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) scur[qb][r] -= up;
+                }
+                acc_fence(oacc);
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                    for (int dt = 0; dt < 4; dt++) acc_scale(oacc[qb][dt], alpha[qb]);
+                acc_fence(oacc);
+            }
+            // V^T fragments of this unit (loaded once half of the K fragments are dead)
+            const int vofs = (3 + ((vb + (u >> 1)) & 1)) * KT_E;
+            bf16x8 vf[2][4];
+            auto load_vf = [&]() __attribute__((always_inline)) {
+#pragma unroll
+                for (int c2 = 0; c2 < 2; c2++)
+#pragma unroll
+                    for (int dt = 0; dt < 4; dt++)
+                        vf[c2][dt] = *reinterpret_cast<const bf16x8*>(
+                            lds + vofs + (vadr[c2] ^ ((u & 1) << 5)) + dt * 32 * TILE);
+            };
+            float (&p)[2][16] = scur;  // exponentials in place
+            f32x16 snx[2];
+            float ps[2] = {0.f, 0.f};
+            if (has_succ) {
+                // ---- phase A: S(u+1) MFMAs with the exponentials of this unit
+                bf16x8 kf[8];
+                const int ko = k_ofs(u + 1);
+#pragma unroll
+                for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
+                // 18 slots: slot 0 / 1 are the bias k-steps of blocks 0 / 1, slot
+                // j >= 2 k-step (j - 2) / 2 of block j & 1; exponentials two per
+                // slot, block 0 in slots 0-7, block 1 in slots 8-15.
+#pragma unroll
+                for (int j = 0; j < 18; j++) {
+                    const int qb = j & 1, st = (j - 2) >> 1;
+                    const int eq = j >> 3, er = 2 * (j & 7);
+                    if (j < 2) exp_qk_first(snx[qb], ones, bfr[qb], p[eq][er], p[eq][er + 1]);
+                    else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
+                    else qk_only(snx[qb], kf[st], qf[qb][st]);
+                    if (j == 9) load_vf();
+                }
+            } else {
+                load_vf();
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) p[qb][r] = __builtin_amdgcn_exp2f(p[qb][r]);
+            }
+            // P^T in the B-operand order of O^T += V^T P^T: element i of
+            // pb[qb][c2] is register 8 c2 + i of S^T[qb]
+            bf16x8 pb[2][2];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                for (int c2 = 0; c2 < 2; c2++)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pb[qb][c2][i] = (__bf16)p[qb][8 * c2 + i];
+            if (has_succ) {
+                mfma_fence_v(snx);
+                const int kvn = unit_kv(u + 1);
+                if (kvn < 32) mask_unit(snx, kvn, hb);
+                // ---- phase B: P.V MFMAs with the row maxima of S(u+1) and the row sums of P(u)
+                float mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int qb = j & 1, dt = (j >> 1) & 3, c2 = j >> 3;  // MFMA
+                    const int eq = j >> 3, er = 2 * (j & 7);                // max / sum items
+                    max_sum_pv(oacc[qb][dt], vf[c2][dt], pb[qb][c2], mx[eq], snx[eq][er], snx[eq][er + 1],
+                               ps[eq], p[eq][er], p[eq][er + 1]);
+                }
+                mtc[0] = max_pair(mx[0]);
+                mtc[1] = max_pair(mx[1]);
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) scur[qb][r] = snx[qb][r];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int qb = j & 1, dt = (j >> 1) & 3, c2 = j >> 3;
+                    const int eq = j >> 3, er = 2 * (j & 7);
+                    sum_pv(oacc[qb][dt], vf[c2][dt], pb[qb][c2], ps[eq], p[eq][er], p[eq][er + 1]);
+                }
+            }
+            l_i[0] += ps[0];
+            l_i[1] += ps[1];
+        };
+
+        // Tile kk issues the DMA of K(kk+2) and V(kk+1) (the last tile: the
+        // next item's first tiles); its second unit ends with the wait for
+        // that DMA and a barrier.  The loop body holds one tile (two units, so
+        // the current and next score registers alternate without copies); the
+        // last tile is peeled because its second unit has no successor.
+        auto tile = [&](int kk, bool last) __attribute__((always_inline)) {
+            if (kk + 2 < nk) dma_k(cur, kk + 2, (kb + kk + 2) % 3);
+            if (kk + 1 < nk) dma_v(cur, kk + 1, (vb + kk + 1) & 1);
+            if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1);
+            if (active) {
+                unit(2 * kk, true);
+                unit(2 * kk + 1, !last);
+            }
+            if (!last) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+        };
+        for (int kk = 0; kk + 1 < nk; kk++) tile(kk, false);
+        tile(nk - 1, true);
+
+        if (active) {
+            acc_fence(oacc);
+            float inv[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) inv[qb] = 1.f / sum_pair(l_i[qb]);
+            const WinTiles wt{cur.vbase, cur.nvt, cur.tbase, a.ntt, cur.f, a.txt_len};
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                bool to_text = false;
+                void* dst = query_dst(a, wt, cur.w, cur.h, kq, 32 * qb + n, to_text, 2);
+                if (dst == nullptr) continue;
+                if (to_text) store_rows<false>(oacc[qb], inv[qb], hb, dst);
+                else store_rows<true>(oacc[qb], inv[qb], hb, dst);
+            }
+        }
+        // the next query tile can load now: this item's Q is dead
+        if (has_next) load_q(nxt);
+        __syncthreads();  // the next item's DMA must not overwrite tiles still read
+        kb = (kb + nk) % 3;
+        vb = (vb + nk) & 1;
+        cur = nxt;
     }
-    if (!active) return;
-    const float l = l_i + __shfl_xor(l_i, 32);
-    const float inv = 1.f / l;
-    bool to_text = false;
-    void* dst = query_dst(a, wt, w, h, kq, qslot, to_text, 2);
-    if (dst == nullptr) return;
-    if (to_text) store_rows<false>(oacc, inv, hb, dst);
-    else store_rows<true>(oacc, inv, hb, dst);
 }
 
 // ----------------------------------------------------------------- fp32
@@ -451,7 +742,7 @@ hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s) {
     const int nblk = a.n_items * HEADS;
     const int grid = ((nblk + 7) >> 3) << 3;
     if (dtype == AWA_BF16)
-        hipLaunchKernelGGL(sdpa_bf16_kernel, dim3(grid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(sdpa_bf16_kernel, dim3(a.n_slots), dim3(128), 0, s, a);
     else
         hipLaunchKernelGGL(sdpa_f32_kernel, dim3(grid), dim3(256), 0, s, a);
     return hipGetLastError();
