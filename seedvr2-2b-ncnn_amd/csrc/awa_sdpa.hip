@@ -157,8 +157,9 @@ __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, 
 //
 // each MFMA and its share of VALU work issued by one asm statement so that
 // the compiler keeps them together.  The output accumulators O^T (128 AGPRs)
-// are pinned to the accumulation registers by the asm constraints; Q and the
-// scores live in VGPRs.  The running maximum m stays stale until a unit's
+// and the query fragments (64 AGPRs, the B operand of the score MFMAs) are
+// pinned to the accumulation registers by the asm constraints; the scores
+// live in VGPRs.  The running maximum m stays stale until a unit's
 // maximum exceeds it by more than 2^8 (the output is divided by the matching
 // sum at the end, so the result is unchanged); then O^T, the running sum and
 // the pending scores are rescaled.  The upper 32-key half of a short last tile
@@ -195,11 +196,15 @@ __device__ inline void exp_qk(f32x16& s, const bf16x8& k, const bf16x8& q, float
         "v_exp_f32 %1, %1\n\tv_exp_f32 %2, %2\n\t"
         "v_mfma_f32_32x32x16_bf16 %0, %3, %4, %0"
         : "+v"(s), "+v"(x0), "+v"(x1)
-        : "v"(k), "v"(q));
+        : "v"(k), "a"(q));
 }
 // A slot without exponentials: s += k q^T.
 __device__ inline void qk_only(f32x16& s, const bf16x8& k, const bf16x8& q) {
-    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(k), "v"(q));
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(k), "a"(q));
+}
+// First MFMA of a chain without exponentials: s = k q^T.
+__device__ inline void qk_zero(f32x16& s, const bf16x8& k, const bf16x8& q) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(k), "a"(q));
 }
 // First MFMA of a score chain: s = k q^T (accumulator from the constant 0).
 __device__ inline void exp_qk_first(f32x16& s, const bf16x8& k, const bf16x8& q, float& x0, float& x1) {
@@ -366,9 +371,20 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // B operand of S^T = K Q^T for column block qb, k-step s:
     // Q[slot 32 qb + n][16 s + 8 hb .. +8]
     bf16x8 qf[2][8];
+    // Output rows of this wave's two query columns, fetched with the query tile
+    // so that the epilogue has no dependent loads: a video row goes to token
+    // vidx[...] of vattn, a text row to the window's partial sums; -1: padding.
+    int orow[2] = {-1, -1};
     auto load_q = [&](const Work& W) __attribute__((always_inline)) {
         const int kq = wave == 0 ? W.q0 : W.q1;
+        orow[0] = orow[1] = -1;
         if (kq < 0) return;
+        const int nvq = kq < W.nvt ? min(TILE, W.f - TILE * kq) : min(TILE, a.txt_len - TILE * (kq - W.nvt));
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            const int slot = 32 * qb + n;
+            if (slot < nvq) orow[qb] = kq < W.nvt ? a.vidx[W.g0 + TILE * kq + slot] : TILE * (kq - W.nvt) + slot;
+        }
         const uint16_t* qt = reinterpret_cast<const uint16_t*>(a.Qp) + W.h * head_stride +
                              (size_t)tile_of(W, kq) * KT_E + 8 * hb;
 #pragma unroll
@@ -402,6 +418,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     for (int wi = wi0; wi < wi1; wi++) {
         const bool has_next = wi + 1 < wi1;
         const Work nxt = load_work(desc, has_next ? wi + 1 : wi);
+        const int orow_cur[2] = {orow[0], orow[1]};
         const int nk = cur.nvt + a.ntt;
         const int kq = wave == 0 ? cur.q0 : cur.q1;
         const bool active = kq >= 0;
@@ -433,15 +450,13 @@ void sdpa_bf16_kernel(SdpaArgs a) {
 #pragma unroll
             for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                f32x16 z;
+            for (int st = 0; st < 8; st++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) z[r] = 0.f;
-                s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[qb][0], z, 0, 0, 0);
-#pragma unroll
-                for (int st = 1; st < 8; st++)
-                    s0[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[qb][st], s0[qb], 0, 0, 0);
-            }
+                for (int qb = 0; qb < 2; qb++) {
+                    if (st == 0) qk_zero(s0[qb], kf[0], qf[qb][0]);
+                    else qk_only(s0[qb], kf[st], qf[qb][st]);
+                }
+            mfma_fence_v(s0);
             const int kv0 = unit_kv(0);
             if (kv0 < 32) mask_unit(s0, kv0, hb);
 #pragma unroll
@@ -510,7 +525,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     if (j < 2) exp_qk_first(snx[qb], ones, bfr[qb], p[eq][er], p[eq][er + 1]);
                     else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
                     else qk_only(snx[qb], kf[st], qf[qb][st]);
-                    if (j == 9) load_vf();
+                    if (j == 3) load_vf();
                 }
             } else {
                 load_vf();
@@ -570,7 +585,12 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1);
             if (active) {
                 unit(2 * kk, true);
+                // the item's last unit computes no scores: Q is dead, so the
+                // next item's query tile loads during it
+                if (last && has_next) load_q(nxt);
                 unit(2 * kk + 1, !last);
+            } else if (last && has_next) {
+                load_q(nxt);
             }
             if (!last) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -585,18 +605,20 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             float inv[2];
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) inv[qb] = 1.f / sum_pair(l_i[qb]);
-            const WinTiles wt{cur.vbase, cur.nvt, cur.tbase, a.ntt, cur.f, a.txt_len};
+            const bool to_text = kq >= cur.nvt;
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) {
-                bool to_text = false;
-                void* dst = query_dst(a, wt, cur.w, cur.h, kq, 32 * qb + n, to_text, 2);
-                if (dst == nullptr) continue;
-                if (to_text) store_rows<false>(oacc[qb], inv[qb], hb, dst);
-                else store_rows<true>(oacc[qb], inv[qb], hb, dst);
+                if (orow_cur[qb] < 0) continue;
+                if (to_text)
+                    store_rows<false>(oacc[qb], inv[qb], hb,
+                                      a.tpart + ((size_t)cur.w * a.txt_len + orow_cur[qb]) * DIM +
+                                          (size_t)cur.h * HEAD_D);
+                else
+                    store_rows<true>(oacc[qb], inv[qb], hb,
+                                     reinterpret_cast<uint16_t*>(a.vattn) + (size_t)orow_cur[qb] * DIM +
+                                         (size_t)cur.h * HEAD_D);
             }
         }
-        // the next query tile can load now: this item's Q is dead
-        if (has_next) load_q(nxt);
         __syncthreads();  // the next item's DMA must not overwrite tiles still read
         kb = (kb + nk) % 3;
         vb = (vb + nk) & 1;
