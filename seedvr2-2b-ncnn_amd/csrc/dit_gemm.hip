@@ -9,11 +9,13 @@
 //
 // Workgroup tile 256 (n) x 256 (m), K step 32, four wave64 in a 2x2 grid of
 // 128x128 wave tiles (16 accumulators per wave).  Operand k-slices reach LDS
-// by direct global->LDS DMA (global_load_lds_dwordx4) into a 4-stage ring
-// (4 x 32 KiB), three stages in flight; the loop waits on the DMA counter
-// with explicit s_waitcnt and a bare s_barrier (a __syncthreads would drain
-// every outstanding load).  Rows are 64 bytes with a 16-byte-chunk XOR
-// swizzle, chunk ^ ((row >> 2) & 3).  Tiles are walked in groups of four
+// by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into a 5-stage
+// ring (5 x 32 KiB, all of LDS), four stages in flight; the loop waits on
+// the DMA counter with explicit s_waitcnt and a bare s_barrier (a
+// __syncthreads would drain every outstanding load).  Rows are 64 bytes with
+// a 16-byte-chunk XOR swizzle, chunk ^ ((row >> 2) & 3).  Each k16 sub-step
+// issues its 16 MFMAs with the next sub-step's fragment reads (and the DMA
+// pieces) one after each of the first eight.  Tiles are walked in groups of four
 // m-tiles and assigned to XCDs in contiguous ranges, so the workgroups
 // resident on one XCD share A and W k-slices through its L2.
 //
@@ -21,6 +23,8 @@
 //   EPI_STORE     C = bf16(acc)                               (qkv)
 //   EPI_RESID     X += gate[n] * (acc + bias[n]), X fp32      (out proj, MLP out)
 //   EPI_SWIGLU    U = bf16(silu(g) * h), W rows interleaved   (proj_in + proj_in_gate)
+#include <type_traits>
+
 #include "dit_internal.hpp"
 
 namespace awa {
@@ -30,11 +34,10 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
 constexpr int BN = 256, BM = 256, BK = 32;
-constexpr int NSTAGE = 4;                 // LDS ring: three K-steps of DMA in flight
+constexpr int NSTAGE = 5;                 // LDS ring (5 x 32 KiB = all of LDS): four K-steps of DMA in flight
 constexpr int ROW_E = BK;                 // bf16 per LDS row (64 B, 4 chunks)
 constexpr int STAGE_E = (BN + BM) * ROW_E;
 
@@ -131,31 +134,38 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     const int hb = lane >> 5, r32 = lane & 31;
 
     // Operand tiles go straight from global memory into LDS
-    // (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
+    // (buffer_load_dwordx4 ... lds: lane i of a wave writes 16 bytes at
     // M0 + 16 i).  One wave instruction fills 1 KiB = 16 swizzled rows; lane l
     // lands in row r0 + l/4, physical chunk l%4, so it fetches the logical
     // chunk that the swizzle maps there.  Each wave issues 4 + 4 per stage.
     const int lrow = lane >> 2;
     const uint16_t* Wp = p.W + (size_t)n0 * p.ldw;
-    const uint16_t* wsrc[4];
-    const uint16_t* asrc[4];
+    // Buffer loads (SGPR resource + 32-bit lane offset + SGPR k offset) issue
+    // measurably faster than global loads with 64-bit lane addresses.  Rows
+    // of A past M repeat the last row; the resource range bounds every read.
+    const uint16_t* Ap = p.A + (size_t)m0 * p.lda;
+    const int arows = min(BM, p.M - m0);
+    int woff[4], aoff[4];   // byte offsets of this lane's 16 bytes at k = 0
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = (wave * 4 + i) * 16 + lrow;
         const int lch = (lane & 3) ^ ((row >> 2) & 3);
-        wsrc[i] = Wp + (size_t)row * p.ldw + lch * 8;
-        asrc[i] = p.A + (size_t)min(m0 + row, p.M - 1) * p.lda + lch * 8;
+        woff[i] = (row * p.ldw + lch * 8) * 2;
+        aoff[i] = (min(row, arows - 1) * p.lda + lch * 8) * 2;
     }
-    auto load = [&](int kt) {
-        uint16_t* ws = lds + (kt % NSTAGE) * STAGE_E;
-        uint16_t* as = ws + BN * ROW_E;
-        const int k0 = kt * BK;
+    // raw buffer, 32-bit dword format (word 3 of the resource)
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc((void*)Wp, 0, BN * p.ldw * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc((void*)Ap, 0, arows * p.lda * 2, 0x00020000);
+    // piece g (0..7) of stage kt into ring slot `slot`: W block g/2 (even g)
+    // or A block g/2 (odd g), 16 rows of 64 bytes
+    auto load_piece = [&](int kt, int slot, int g) __attribute__((always_inline)) {
+        uint16_t* dst = lds + slot * STAGE_E + ((g & 1) ? BN * ROW_E : 0) + (wave * 4 + (g >> 1)) * 512;
+        if (g & 1) __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lptr_t)dst, 16, aoff[g >> 1], kt * BK * 2, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lptr_t)dst, 16, woff[g >> 1], kt * BK * 2, 0, 0);
+    };
+    auto load = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int blk = wave * 4 + i;
-            __builtin_amdgcn_global_load_lds((gptr_t)(wsrc[i] + k0), (lptr_t)(ws + blk * 512), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gptr_t)(asrc[i] + k0), (lptr_t)(as + blk * 512), 16, 0, 0);
-        }
+        for (int g = 0; g < 8; g++) load_piece(kt, slot, g);
     };
 
     f32x16 acc[4][4];
@@ -167,53 +177,83 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const int nk = p.K / BK;
-    // prologue: stages 0..2 in flight, wait for stage 0
-#pragma unroll
-    for (int s0 = 0; s0 < NSTAGE - 1; s0++)
-        if (s0 < nk) load(s0);
-    if (nk >= 3) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (nk == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // A bare barrier: __syncthreads() would also drain the DMA prefetch.
-    __builtin_amdgcn_s_barrier();
-
     int wrow[4], arow[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         wrow[i] = wn * 128 + 32 * i + r32;
         arow[i] = wm * 128 + 32 * i + r32;
     }
-    for (int kt = 0; kt < nk; kt++) {
-        if (kt + NSTAGE - 1 < nk) load(kt + NSTAGE - 1);
-        const uint16_t* ws = lds + (kt % NSTAGE) * STAGE_E;
+    // fragments of one k16 sub-step: four 32-row blocks of W and of A
+    bf16x8 wf[2][4], af[2][4];
+    // slot `slot`, k16 sub-step s, fragment buffer buf
+    auto read_frags = [&](int slot, int s, int buf) __attribute__((always_inline)) {
+        const uint16_t* ws = lds + slot * STAGE_E;
         const uint16_t* as = ws + BN * ROW_E;
-        // two k16 steps; fragments of both are read before the MFMAs
-        bf16x8 wf[2][4], af[2][4];
 #pragma unroll
-        for (int s = 0; s < 2; s++)
+        for (int i = 0; i < 4; i++) {
+            wf[buf][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 2 * s + hb));
+            af[buf][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 2 * s + hb));
+        }
+    };
+    // One k16 sub-step: the 16 MFMAs on fragment buffer `buf`; after each of
+    // the first eight, one fragment read of the next sub-step (slot rslot,
+    // sub-step rs, into buffer buf ^ 1) and, when `dma`, one DMA piece of
+    // stage dma_kt.  sched_barrier pins this order: every read is in
+    // flight half a sub-step before its use, the wait for the previous
+    // sub-step's reads comes before the first new read (the compiler waits
+    // on the LDS counter with lgkmcnt(0)), and the DMA issue is spread out.
+    auto substep = [&](int buf, int rslot, int rs, bool do_read, bool dma, int dma_kt, int dma_slot)
+        __attribute__((always_inline)) {
+        const uint16_t* ws = lds + rslot * STAGE_E;
+        const uint16_t* as = ws + BN * ROW_E;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                wf[s][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 2 * s + hb));
-                af[s][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 2 * s + hb));
+        for (int g = 0; g < 16; g++) {
+            const int i = g >> 2, j = g & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
+            if (g < 8) {
+                if (dma) load_piece(dma_kt, dma_slot, g);
+                if (do_read) {
+                    const int r = g >> 1;
+                    if (g & 1)
+                        af[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(as + swz(arow[r], 2 * rs + hb));
+                    else
+                        wf[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[r], 2 * rs + hb));
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Software pipeline over k16 sub-steps: the fragments of the next
+    // sub-step are read beside the 16 MFMAs of the current one.  Between the
+    // two sub-steps of stage kt: wait until stage kt+1 has landed and this
+    // wave's LDS reads are complete, barrier (every wave then has stage kt+1,
+    // and no wave still reads stage kt-1), refill stage kt-1's slot with stage
+    // kt+3.  Past the last stage the refill repeats stage nk-1 into the freed
+    // slot, which is never read again: the loop body stays branch-free and
+    // the DMA count it waits on stays fixed.
+    const int last = nk - 1;
 #pragma unroll
-        for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[s][i], af[s][j], acc[i][j], 0, 0, 0);
-        // schedule: the 16 fragment reads first, then the 32 MFMAs back to back
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
-        // stage kt+1 must have landed; younger stages may still be in flight
-        const int ahead = min(nk - 1 - kt, NSTAGE - 1);  // stages issued after kt
-        // (this wave's LDS reads of stage kt are complete: the MFMAs consumed them)
-        if (ahead >= 3) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
-        else if (ahead == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    for (int s0 = 0; s0 < NSTAGE - 1; s0++) load(min(s0, last), s0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (NSTAGE - 2)) : "memory");
+    // A bare barrier: __syncthreads() would also drain the DMA prefetch.
+    __builtin_amdgcn_s_barrier();
+    read_frags(0, 0, 0);
+    int slot = 0;
+    for (int kt = 0; kt < last; kt++) {
+        const int nslot = slot == NSTAGE - 1 ? 0 : slot + 1;
+        substep(0, slot, 1, true, false, 0, 0);
+        // stage kt+1 landed; stages kt+2 .. kt+NSTAGE-2 may still fly.  The
+        // reads of the slot refilled below (stage kt-1) were consumed by the
+        // MFMAs of the previous step, so no LDS wait is needed here.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (NSTAGE - 3)) : "memory");
         __builtin_amdgcn_s_barrier();
+        substep(1, nslot, 0, true, true, min(kt + NSTAGE - 1, last), slot == 0 ? NSTAGE - 1 : slot - 1);
+        slot = nslot;
     }
+    substep(0, slot, 1, true, false, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    substep(1, 0, 0, false, false, 0, 0);
     epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane);
 }
 
