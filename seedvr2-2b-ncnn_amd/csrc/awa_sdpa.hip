@@ -305,9 +305,13 @@ __device__ inline void mask_unit(f32x16 (&s)[2], int kvalid, int hb) {
 struct Work {
     int h, w, q0, q1, g0, vbase, nvt, tbase, f;
 };
-__device__ inline Work load_work(const int4* d, int i) {
-    const int4 x = d[2 * i], y = d[2 * i + 1];
-    return Work{x.x & 255, x.x >> 8, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+// The descriptors are read through the constant address space, so that the
+// uniform loads become scalar loads, waited on by lgkmcnt rather than by the
+// vector-memory counter that also counts the output stores.
+typedef __attribute__((address_space(4))) const int32_t cint32;
+__device__ inline Work load_work(cint32* d, int i) {
+    cint32* e = d + 8 * i;
+    return Work{e[0] & 255, e[0] >> 8, e[1], e[2], e[3], e[4], e[5], e[6], e[7]};
 }
 
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -315,7 +319,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     __shared__ __align__(16) uint16_t lds[5 * KT_E];  // K ring (3 tile slots), V^T ring (2 slots)
     const int wi0 = a.sched_start[blockIdx.x], wi1 = a.sched_start[blockIdx.x + 1];
     if (wi0 >= wi1) return;
-    const int4* desc = reinterpret_cast<const int4*>(a.sched_desc);
+    cint32* desc = (cint32*)(a.sched_desc);
 
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -375,23 +379,34 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // so that the epilogue has no dependent loads: a video row goes to token
     // vidx[...] of vattn, a text row to the window's partial sums; -1: padding.
     int orow[2] = {-1, -1};
+    // The fragments are loaded on every path (an idle wave loads its
+    // partner's tile and leaves orow at -1), so that the new fragments can
+    // take the registers of the dead ones: a conditional load keeps the old
+    // values alive, and the register copies that follows wait for the load.
     auto load_q = [&](const Work& W) __attribute__((always_inline)) {
         const int kq = wave == 0 ? W.q0 : W.q1;
-        orow[0] = orow[1] = -1;
-        if (kq < 0) return;
-        const int nvq = kq < W.nvt ? min(TILE, W.f - TILE * kq) : min(TILE, a.txt_len - TILE * (kq - W.nvt));
+        const int kql = kq < 0 ? W.q0 : kq;
+        const int nvq = kq < 0 ? 0
+                      : kq < W.nvt ? min(TILE, W.f - TILE * kq) : min(TILE, a.txt_len - TILE * (kq - W.nvt));
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {
             const int slot = 32 * qb + n;
+            orow[qb] = -1;
             if (slot < nvq) orow[qb] = kq < W.nvt ? a.vidx[W.g0 + TILE * kq + slot] : TILE * (kq - W.nvt) + slot;
         }
         const uint16_t* qt = reinterpret_cast<const uint16_t*>(a.Qp) + W.h * head_stride +
-                             (size_t)tile_of(W, kq) * KT_E + 8 * hb;
+                             (size_t)tile_of(W, kql) * KT_E + 8 * hb;
+        // Loaded by asm straight into the fragment registers: the compiler
+        // neither waits for these loads where it would copy them (it sees
+        // no load) nor may it move them; the wait for them is the item
+        // start's s_waitcnt vmcnt(0).
 #pragma unroll
-        for (int qb = 0; qb < 2; qb++)
+        for (int qb = 0; qb < 2; qb++) {
+            const uint16_t* row = qt + (32 * qb + n) * HEAD_D;
 #pragma unroll
             for (int s = 0; s < 8; s++)
-                qf[qb][s] = *reinterpret_cast<const bf16x8*>(qt + (32 * qb + n) * HEAD_D + 16 * s);
+                asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=a"(qf[qb][s]) : "v"(row), "n"(32 * s));
+        }
     };
 
     // LDS fragment addresses.  K fragment (k-step s) of a unit: row n of the
@@ -583,15 +598,12 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             if (kk + 2 < nk) dma_k(cur, kk + 2, (kb + kk + 2) % 3);
             if (kk + 1 < nk) dma_v(cur, kk + 1, (vb + kk + 1) & 1);
             if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1);
-            if (active) {
-                unit(2 * kk, true);
-                // the item's last unit computes no scores: Q is dead, so the
-                // next item's query tile loads during it
-                if (last && has_next) load_q(nxt);
-                unit(2 * kk + 1, !last);
-            } else if (last && has_next) {
-                load_q(nxt);
-            }
+            if (active) unit(2 * kk, true);
+            // the item's last unit computes no scores: Q is dead, so the
+            // next item's query tile loads during it (after the slot's last
+            // item: the same tile again, unused)
+            if (last) load_q(nxt);
+            if (active) unit(2 * kk + 1, !last);
             if (!last) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
@@ -600,26 +612,59 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         for (int kk = 0; kk + 1 < nk; kk++) tile(kk, false);
         tile(nk - 1, true);
 
+        // Item epilogue.  Text rows (fp32 partials) are stored straight from
+        // the accumulators.  Video rows go through LDS: once both waves are
+        // done with the last tile, its K slot (wave 0) and V slot (wave 1)
+        // are free, so each wave writes its normalised bf16 tile there
+        // (16-byte chunk c of row r at chunk c ^ (r & 15)) and reads it back
+        // as whole 256-byte rows, four rows per store instruction.  Stores of
+        // 16-byte pieces of 32 rows each cost the memory system far more than
+        // the same bytes in whole lines.  The next item's start (wait and
+        // barrier) keeps its DMA out of these slots until both waves have
+        // read them back.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
         if (active) {
             acc_fence(oacc);
             float inv[2];
 #pragma unroll
             for (int qb = 0; qb < 2; qb++) inv[qb] = 1.f / sum_pair(l_i[qb]);
-            const bool to_text = kq >= cur.nvt;
+            if (kq >= cur.nvt) {
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                if (orow_cur[qb] < 0) continue;
-                if (to_text)
+                for (int qb = 0; qb < 2; qb++) {
+                    if (orow_cur[qb] < 0) continue;
                     store_rows<false>(oacc[qb], inv[qb], hb,
                                       a.tpart + ((size_t)cur.w * a.txt_len + orow_cur[qb]) * DIM +
                                           (size_t)cur.h * HEAD_D);
-                else
-                    store_rows<true>(oacc[qb], inv[qb], hb,
-                                     reinterpret_cast<uint16_t*>(a.vattn) + (size_t)orow_cur[qb] * DIM +
-                                         (size_t)cur.h * HEAD_D);
+                }
+            } else {
+                uint16_t* stg = lds + (wave == 0 ? (kb + nk - 1) % 3 : 3 + ((vb + nk - 1) & 1)) * KT_E;
+#pragma unroll
+                for (int qb = 0; qb < 2; qb++) {
+                    const int row = 32 * qb + n;
+#pragma unroll
+                    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++) {
+                            const f32x16& o = oacc[qb][dt];
+                            const float iv = inv[qb];
+                            uint2 u;
+                            u.x = bf16_rne(o[4 * g] * iv) | (bf16_rne(o[4 * g + 1] * iv) << 16);
+                            u.y = bf16_rne(o[4 * g + 2] * iv) | (bf16_rne(o[4 * g + 3] * iv) << 16);
+                            const int c = 4 * dt + g;
+                            *reinterpret_cast<uint2*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3) + 4 * hb) = u;
+                        }
+                }
+                uint16_t* out = reinterpret_cast<uint16_t*>(a.vattn) + (size_t)cur.h * HEAD_D + (lane & 15) * 8;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int row = 4 * i + (lane >> 4), c = lane & 15;
+                    const int tok = __shfl(orow_cur[i >> 3], row & 31);
+                    const uint4 v = *reinterpret_cast<const uint4*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3));
+                    if (tok >= 0) *reinterpret_cast<uint4*>(out + (size_t)tok * DIM) = v;
+                }
             }
         }
-        __syncthreads();  // the next item's DMA must not overwrite tiles still read
         kb = (kb + nk) % 3;
         vb = (vb + nk) & 1;
         cur = nxt;
