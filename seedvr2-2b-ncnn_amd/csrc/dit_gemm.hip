@@ -47,19 +47,54 @@ constexpr int STAGE_E = (BN + BM) * ROW_E;
 __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 2) & 3)) << 3); }
 
 
+// Epilogues go through LDS so that global memory sees whole rows: stores of
+// 8- or 16-byte pieces of 32 rows per instruction (the accumulator layout)
+// cost the memory system several times what whole 128-byte lines do.  Each
+// wave stages its 128 x 128 block in its own 32 KiB of LDS as rows of the
+// output (16-byte chunk c of staged row r at chunk c ^ (r & (chunks - 1)),
+// conflict-free for both the accumulator-order writes and the row reads) and
+// reads it back row by row, 16 (or 8) lanes per row.
+//
+// Accumulator layout: acc[i][j] is the 32x32 block of output features
+// n_base + 32 i + .. and rows m_base + 32 j + ..; lane (col = lane % 32,
+// hb = lane / 32) holds row 32 j + col, features 32 i + 8 g + 4 hb + t in
+// register 4 g + t.
 template <int EPI>
 __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4], int n_base,
-                                int m_base, int lane) {
+                                int m_base, int lane, uint16_t* stg) {
     const int hb = lane >> 5, col = lane & 31;
+    if constexpr (EPI == EPI_STORE) {
+        // staged rows: 128 features bf16 = 256 bytes, 16 chunks
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int m = m_base + 32 * j + col;
-        if (m >= p.M) continue;
-        if constexpr (EPI == EPI_SWIGLU) {
-            // blocks (0,1) and (2,3): (in, gate) of feature groups q and q+1
+        for (int j = 0; j < 4; j++) {
+            const int r = 32 * j + col;
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
-                const int fbase = (n_base >> 1) + 32 * q;
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const f32x16& a = acc[i][j];
+                    const uint2 u = make_uint2(bf16_rne(a[4 * g]) | (bf16_rne(a[4 * g + 1]) << 16),
+                                               bf16_rne(a[4 * g + 2]) | (bf16_rne(a[4 * g + 3]) << 16));
+                    const int c = 4 * i + g;
+                    *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ (r & 15)) << 3) + 4 * hb) = u;
+                }
+        }
+        const int c = lane & 15;
+        uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + n_base + c * 8;
+#pragma unroll 8
+        for (int it = 0; it < 32; it++) {
+            const int r = 4 * it + (lane >> 4), m = m_base + r;
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 128 + ((c ^ (r & 15)) << 3));
+            if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
+        }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // blocks (0,1) and (2,3): (in, gate) of output features 32 q + ..;
+        // staged rows: 64 features bf16 = 128 bytes, 8 chunks
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = 32 * j + col;
+#pragma unroll
+            for (int q = 0; q < 2; q++)
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
                     uint32_t packed[2];
@@ -74,39 +109,60 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4],
                         }
                         packed[e >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
                     }
-                    const int f = fbase + 8 * g + 4 * hb;
-                    uint16_t* dst = reinterpret_cast<uint16_t*>(p.C) + (size_t)m * p.ldc + f;
-                    *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+                    const int c = 4 * q + g;
+                    *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ (r & 7)) << 3) + 4 * hb) =
+                        make_uint2(packed[0], packed[1]);
+                }
+        }
+        const int c = lane & 7;
+        uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + (n_base >> 1) + c * 8;
+#pragma unroll 8
+        for (int it = 0; it < 16; it++) {
+            const int r = 8 * it + (lane >> 3), m = m_base + r;
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 64 + ((c ^ (r & 7)) << 3));
+            if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
+        }
+    } else {  // EPI_RESID, in two halves of 64 features (staged fp32 rows: 256 bytes)
+        float* sf = reinterpret_cast<float*>(stg);
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = 32 * j + col;
+#pragma unroll
+                for (int i2 = 0; i2 < 2; i2++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const f32x16& a = acc[2 * half + i2][j];
+                        const int c = 8 * i2 + 2 * g + hb;
+                        *reinterpret_cast<float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2)) =
+                            make_float4(a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
+                    }
+            }
+            const int c = lane & 15;
+            const int n = n_base + 64 * half + 4 * c;
+            float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n);
+            const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);
+            const float4 g0 = p.gate0 ? *reinterpret_cast<const float4*>(p.gate0 + n) : one;
+            const float4 g1 = p.gate1 ? *reinterpret_cast<const float4*>(p.gate1 + n) : one;
+            float* out = reinterpret_cast<float*>(p.C) + n;
+#pragma unroll 8
+            for (int it = 0; it < 32; it++) {
+                const int r = 4 * it + (lane >> 4), m = m_base + r;
+                const float4 v = *reinterpret_cast<const float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2));
+                if (m < p.M) {
+                    const float4 gt = m < p.split ? g0 : g1;
+                    float4* dst = reinterpret_cast<float4*>(out + (size_t)m * p.ldc);
+                    float4 x = *dst;
+                    // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
+                    x.x = gt.x * (v.x + b.x) + x.x;
+                    x.y = gt.y * (v.y + b.y) + x.y;
+                    x.z = gt.z * (v.z + b.z) + x.z;
+                    x.w = gt.w * (v.w + b.w) + x.w;
+                    *dst = x;
                 }
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const int n = n_base + 32 * i + 8 * g + 4 * hb;
-                    const float a0 = acc[i][j][4 * g], a1 = acc[i][j][4 * g + 1];
-                    const float a2 = acc[i][j][4 * g + 2], a3 = acc[i][j][4 * g + 3];
-                    if constexpr (EPI == EPI_STORE) {
-                        uint16_t* dst = reinterpret_cast<uint16_t*>(p.C) + (size_t)m * p.ldc + n;
-                        *reinterpret_cast<uint2*>(dst) =
-                            make_uint2(bf16_rne(a0) | (bf16_rne(a1) << 16), bf16_rne(a2) | (bf16_rne(a3) << 16));
-                    } else {  // EPI_RESID
-                        float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-                        if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n);
-                        const float* gp = m < p.split ? p.gate0 : p.gate1;
-                        float4 gt = make_float4(1.f, 1.f, 1.f, 1.f);
-                        if (gp) gt = *reinterpret_cast<const float4*>(gp + n);
-                        float* dst = reinterpret_cast<float*>(p.C) + (size_t)m * p.ldc + n;
-                        float4 x = *reinterpret_cast<float4*>(dst);
-                        // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
-                        x.x = gt.x * (a0 + b.x) + x.x;
-                        x.y = gt.y * (a1 + b.y) + x.y;
-                        x.z = gt.z * (a2 + b.z) + x.z;
-                        x.w = gt.w * (a3 + b.w) + x.w;
-                        *reinterpret_cast<float4*>(dst) = x;
-                    }
-                }
         }
     }
 }
@@ -254,7 +310,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     substep(0, slot, 1, true, false, 0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     substep(1, 0, 0, false, false, 0, 0);
-    epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane);
+    // every wave is done with the operand tiles: LDS becomes the staging area
+    __syncthreads();
+    epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane, lds + wave * (128 * 128));
 }
 
 }  // namespace
