@@ -29,6 +29,17 @@ METRIC = "1080p bf16 AWA-layer ms & MFMA util; 32-layer DiT step sec; 1 GPU"
 GRID, NUM_WINDOWS, TXT, SEED = (1, 68, 80), (4, 3, 3), 58, 2
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE, WRITE_SIZE,
+# calibrated against a plain copy); the counters need a profiler run of their own.
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def measured_traffic():
+    try:
+        with open(TRAFFIC_JSON) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
 
 
 def sdpa_flops(S_list):
@@ -226,6 +237,9 @@ def main():
     # memory-bound pass: qk-norm + RoPE, algorithmic bytes = read + write q and k
     qk_bytes = 2 * (Lv + TXT) * 2 * 2560 * 2
     pack_avg_s = ms_pack * 1e-3 / calls
+    traffic = measured_traffic()
+    sdpa_bytes = traffic.get("sdpa_bf16_kernel", {}).get("total_bytes")
+    pack_bytes = traffic.get("pack_kernel", {}).get("total_bytes")
 
     out = {
         "metric": METRIC,
@@ -245,7 +259,8 @@ def main():
                    "steps_alternate": "unshifted (16 windows) / shifted (25 windows)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "sdpa_bf16_kernel",
+                     "traffic": sdpa_bytes, "traffic_unit": "bytes per launch (rocprofv3 PMC)",
+                     "kernel": "sdpa_bf16_kernel",
                      "avg_launch_us": round(attn_avg_s * 1e6, 2),
                      "algorithmic_gflop_per_launch": round(flops_timed / calls / 1e9, 3)},
         "phases_us": {"pack_qknorm_rope": round(pack_avg_s * 1e6, 2),
@@ -253,7 +268,9 @@ def main():
                       "text_average": round(ms_text * 1e3 / calls, 2)},
         "hbm_qknorm_rope": {"algorithmic_bytes": qk_bytes,
                             "achieved_GBs": round(qk_bytes / pack_avg_s / 1e9, 1),
-                            "frac": round(qk_bytes / pack_avg_s / 1e9 / PEAK_HBM_GBS, 4)},
+                            "frac": round(qk_bytes / pack_avg_s / 1e9 / PEAK_HBM_GBS, 4),
+                            "measured_bytes": pack_bytes,
+                            "measured_GBs": round(pack_bytes / pack_avg_s / 1e9, 1) if pack_bytes else None},
         "per_variant": per_variant,
     }
     if not args.no_dit:
