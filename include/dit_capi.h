@@ -84,6 +84,43 @@ int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb,
 int dit_timing_read(awa_ctx* ctx, double* ms_gemm, double* ms_awa, double* ms_eltwise,
                     int* layers);
 
+/* The DiT's input and output layers (DitVk::forward_grid, dit_vk.cpp:752-763,
+ * with forward_latent's vid_in_proj / txt_in, dit_vk.cpp:494-497, and its final
+ * norm, ada and vid_out_proj, dit_vk.cpp:657-675).  Linear weights [out][in]
+ * as the reference's InnerProduct layers (verify_dit.cpp:354-356: all three
+ * with bias), bf16 on the device; vectors fp32. */
+typedef struct {
+    const uint16_t* vid_in_w;     /* bf16 [2560][132], input in (ph, pw, c) patch order */
+    const float* vid_in_b;        /* fp32 [2560]                                        */
+    const uint16_t* txt_in_w;     /* bf16 [2560][5120]                                  */
+    const float* txt_in_b;        /* fp32 [2560]                                        */
+    const float* out_norm_w;      /* fp32 [2560] vid_out_norm_w (RMSNorm weight)        */
+    const float* out_ada_shift;   /* fp32 [2560] vid_out_ada_shift                      */
+    const float* out_ada_scale;   /* fp32 [2560] vid_out_ada_scale                      */
+    const uint16_t* vid_out_w;    /* bf16 [64][2560] vid_out_proj                       */
+    const float* vid_out_b;       /* fp32 [64]                                          */
+} dit_io_weights;
+
+/* Prepared input/output layers: padded device copies of vid_in_w (K 132 ->
+ * 160) and vid_out_w / vid_out_b (N 64 -> 256) for the block's GEMM kernel;
+ * the other pointers are borrowed and must stay valid. */
+typedef struct dit_io dit_io;
+int dit_io_create(awa_ctx* ctx, const dit_io_weights* w, dit_io** out, awa_stream_t stream);
+void dit_io_destroy(awa_ctx* ctx, dit_io* io);
+
+/* Input layers: patchify the latent grid d_grid fp32 (T, H, W, 33) (H, W even;
+ * dit_vk.cpp:717-733), vid_in_proj to the video rows and txt_in of d_txt fp32
+ * [TXT][5120] to the text rows of the residual stream d_x fp32
+ * [Lv + TXT][2560], Lv = T (H/2) (W/2).  bf16 GEMM inputs, fp32 out. */
+int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H, int W,
+              const float* d_txt, int TXT, float* d_x, awa_stream_t stream);
+
+/* Output layer: RMSNorm of the video rows of d_x with out_norm_w, times
+ * (emb[6d+1] + out_ada_scale) plus (emb[6d] + out_ada_shift), vid_out_proj,
+ * unpatchified to d_out fp32 (T, H, W, 16) (dit_vk.cpp:735-750). */
+int dit_final(awa_ctx* ctx, const dit_io* io, const float* d_emb, const float* d_x, int T, int H,
+              int W, float eps, float* d_out, awa_stream_t stream);
+
 /* Plain bf16 GEMM with the block's kernel, for tests and measurement:
  * C[M][N] = A[M][K] W[N][K]^T, bf16 in, bf16 out (fp32 accumulation).
  * N a multiple of 256, K a multiple of 64. */

@@ -38,6 +38,15 @@ class DitBranch(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in BRANCH_FIELDS]
 
 
+IO_FIELDS = ("vid_in_w", "vid_in_b", "txt_in_w", "txt_in_b", "out_norm_w", "out_ada_shift",
+             "out_ada_scale", "vid_out_w", "vid_out_b")
+
+
+class DitIoWeights(C.Structure):
+    """dit_io_weights of include/dit_capi.h (device pointers)."""
+    _fields_ = [(n, C.c_void_p) for n in IO_FIELDS]
+
+
 class GeomInfo(C.Structure):
     _fields_ = [(n, C.c_int32) for n in
                 ("t", "h", "w", "nwin", "sumf", "Lv", "txt_len", "max_S", "n_tiles", "n_items")]
@@ -89,6 +98,11 @@ def lib():
         L.dit_timing_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                       C.POINTER(C.c_double), C.POINTER(C.c_int)]
         L.dit_gemm_bf16.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]
+        L.dit_io_create.argtypes = [vp, C.POINTER(DitIoWeights), C.POINTER(vp), vp]
+        L.dit_io_destroy.argtypes = [vp, vp]
+        L.dit_io_destroy.restype = None
+        L.dit_embed.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, vp]
+        L.dit_final.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, vp]
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
@@ -265,6 +279,37 @@ class Context:
         self.check(rc, "dit_layer_forward")
         return x
 
+    def io_layers(self, weights, stream=None):
+        """dit_io_create from a dict of device tensors keyed like dit_io_weights; the
+        returned object keeps the tensors alive (the handle borrows some of them)."""
+        w = DitIoWeights(**{k: weights[k].data_ptr() for k in IO_FIELDS})
+        h = C.c_void_p()
+        self.check(lib().dit_io_create(self.ptr, C.byref(w), C.byref(h), _stream_ptr(stream)), "dit_io_create")
+        return DitIo(self, h, weights)
+
+    def embed(self, io, grid, txt, x=None, stream=None):
+        """dit_embed: grid fp32 (T, H, W, 33), txt fp32 [TXT, 5120] -> x fp32 [Lv+TXT, 2560]."""
+        import torch
+        T, H, W, _ = grid.shape
+        TXT = txt.shape[0]
+        Lv = T * (H // 2) * (W // 2)
+        if x is None:
+            x = torch.empty((Lv + TXT, DIM), dtype=torch.float32, device=grid.device)
+        rc = lib().dit_embed(self.ptr, io.ptr, C.c_void_p(grid.data_ptr()), int(T), int(H), int(W),
+                             C.c_void_p(txt.data_ptr()), int(TXT), C.c_void_p(x.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_embed")
+        return x
+
+    def final(self, io, emb, x, T, H, W, eps=1e-5, out=None, stream=None):
+        """dit_final: video rows of x -> fp32 (T, H, W, 16)."""
+        import torch
+        if out is None:
+            out = torch.empty((T, H, W, 16), dtype=torch.float32, device=x.device)
+        rc = lib().dit_final(self.ptr, io.ptr, C.c_void_p(emb.data_ptr()), C.c_void_p(x.data_ptr()), int(T),
+                             int(H), int(W), float(eps), C.c_void_p(out.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_final")
+        return out
+
     def dit_timing_read(self):
         a, b, c = C.c_double(), C.c_double(), C.c_double()
         n = C.c_int()
@@ -314,6 +359,24 @@ class Geometry:
         if self.ptr:
             lib().awa_geom_destroy(self.ptr)
             self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DitIo:
+    """Handle of dit_io_create; destroyed with the object."""
+
+    def __init__(self, ctx, ptr, weights):
+        self.ctx, self.ptr, self._weights = ctx, ptr, weights
+
+    def close(self):
+        if self.ptr:
+            lib().dit_io_destroy(self.ctx.ptr, self.ptr)
+            self.ptr = None
 
     def __del__(self):
         try:

@@ -35,9 +35,130 @@ GemmProblem problem(const uint16_t* A, int lda, const uint16_t* W, int ldw, int 
     return p;
 }
 
+constexpr int VID_IN = 132, VID_IN_PAD = 160;   // patch channels 33 x 2 x 2; K padded to the GEMM step
+constexpr int VID_OUT = 64, VID_OUT_PAD = 256;  // output channels 16 x 2 x 2; N padded to the GEMM tile
+
 }  // namespace
 
+struct dit_io {
+    int device = 0;
+    uint16_t* vid_in_w = nullptr;   // [2560][160], columns 132.. zero
+    const float* vid_in_b = nullptr;
+    const uint16_t* txt_in_w = nullptr;
+    const float* txt_in_b = nullptr;
+    const float* out_norm_w = nullptr;
+    const float* out_ada_shift = nullptr;
+    const float* out_ada_scale = nullptr;
+    uint16_t* vid_out_w = nullptr;  // [256][2560], rows 64.. zero
+    float* vid_out_b = nullptr;     // [256], 64.. zero
+};
+
 extern "C" {
+
+int dit_io_create(awa_ctx* ctx, const dit_io_weights* w, dit_io** out, awa_stream_t stream) {
+    if (!ctx || !w || !out || !w->vid_in_w || !w->vid_in_b || !w->txt_in_w || !w->txt_in_b ||
+        !w->out_norm_w || !w->out_ada_shift || !w->out_ada_scale || !w->vid_out_w || !w->vid_out_b) {
+        set_err(ctx, "dit_io_create: null argument");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    dit_io* io = new dit_io();
+    io->device = ctx->device;
+    io->vid_in_b = w->vid_in_b; io->txt_in_w = w->txt_in_w; io->txt_in_b = w->txt_in_b;
+    io->out_norm_w = w->out_norm_w; io->out_ada_shift = w->out_ada_shift; io->out_ada_scale = w->out_ada_scale;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&io->vid_in_w), (size_t)DIM * VID_IN_PAD * 2);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&io->vid_out_w), (size_t)VID_OUT_PAD * DIM * 2);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&io->vid_out_b), VID_OUT_PAD * 4);
+    // zero, then copy the real rows / columns in (set-up, not in a captured sequence)
+    if (e == hipSuccess) e = hipMemsetAsync(io->vid_in_w, 0, (size_t)DIM * VID_IN_PAD * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(io->vid_out_w, 0, (size_t)VID_OUT_PAD * DIM * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(io->vid_out_b, 0, VID_OUT_PAD * 4, s);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(io->vid_in_w, VID_IN_PAD * 2, w->vid_in_w, VID_IN * 2, VID_IN * 2, DIM,
+                             hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(io->vid_out_w, w->vid_out_w, (size_t)VID_OUT * DIM * 2, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(io->vid_out_b, w->vid_out_b, VID_OUT * 4, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) {
+        set_err(ctx, "dit_io_create: %s", hipGetErrorString(e));
+        dit_io_destroy(ctx, io);
+        return AWA_EHIP;
+    }
+    *out = io;
+    return AWA_OK;
+}
+
+void dit_io_destroy(awa_ctx* ctx, dit_io* io) {
+    if (!io) return;
+    DeviceGuard dg(ctx ? ctx->device : io->device);
+    if (io->vid_in_w) (void)hipFree(io->vid_in_w);
+    if (io->vid_out_w) (void)hipFree(io->vid_out_w);
+    if (io->vid_out_b) (void)hipFree(io->vid_out_b);
+    delete io;
+}
+
+int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H, int W, const float* d_txt,
+              int TXT, float* d_x, awa_stream_t stream) {
+    if (!ctx || !io || !d_grid || !d_txt || !d_x || T < 1 || H < 2 || W < 2 || H % 2 || W % 2 || TXT < 1) {
+        set_err(ctx, "dit_embed: bad argument (T=%d H=%d W=%d TXT=%d; H and W even)", T, H, W, TXT);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int Lv = T * (H / 2) * (W / 2), M = Lv + TXT;
+    // workspace: patches [Lv][160] bf16 | text [TXT][5120] bf16
+    const size_t o_t = align256((size_t)Lv * VID_IN_PAD * 2);
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, o_t + align256((size_t)TXT * 5120 * 2)));
+    uint16_t* patch = static_cast<uint16_t*>(ctx->ws);
+    uint16_t* txt = reinterpret_cast<uint16_t*>(static_cast<char*>(ctx->ws) + o_t);
+    HIPCK(ctx, launch_patchify(d_grid, T, H, W, patch, VID_IN_PAD, s));
+    HIPCK(ctx, launch_cast_f32_bf16(d_txt, txt, (int64_t)TXT * 5120, s));
+    // x = A W^T + b: the residual epilogue on a zeroed x, gate 1
+    HIPCK(ctx, launch_zero(d_x, (size_t)M * DIM * 4, s));
+    GemmBatch b{};
+    b.nprob = 2;
+    b.p[0] = problem(patch, VID_IN_PAD, io->vid_in_w, VID_IN_PAD, Lv, DIM, VID_IN_PAD, d_x, DIM);
+    b.p[0].bias = io->vid_in_b;
+    b.p[1] = problem(txt, 5120, io->txt_in_w, 5120, TXT, DIM, 5120, d_x + (size_t)Lv * DIM, DIM);
+    b.p[1].bias = io->txt_in_b;
+    HIPCK(ctx, launch_gemm(EPI_RESID, b, s));
+    return AWA_OK;
+}
+
+int dit_final(awa_ctx* ctx, const dit_io* io, const float* d_emb, const float* d_x, int T, int H, int W,
+              float eps, float* d_out, awa_stream_t stream) {
+    if (!ctx || !io || !d_emb || !d_x || !d_out || T < 1 || H < 2 || W < 2 || H % 2 || W % 2 || !(eps > 0.f)) {
+        set_err(ctx, "dit_final: bad argument (T=%d H=%d W=%d; H and W even, eps > 0)", T, H, W);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int Lv = T * (H / 2) * (W / 2);
+    // workspace: scale, shift [2][2560] f32 | h [Lv][2560] bf16 | y [Lv][256] f32
+    const size_t o_h = align256(2 * DIM * 4);
+    const size_t o_y = o_h + align256((size_t)Lv * DIM * 2);
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, o_y + align256((size_t)Lv * VID_OUT_PAD * 4)));
+    char* ws = static_cast<char*>(ctx->ws);
+    float* scale = reinterpret_cast<float*>(ws);
+    float* shift = scale + DIM;
+    uint16_t* h = reinterpret_cast<uint16_t*>(ws + o_h);
+    float* y = reinterpret_cast<float*>(ws + o_y);
+    HIPCK(ctx, launch_final_ada(d_emb, io->out_norm_w, io->out_ada_scale, io->out_ada_shift, scale, shift, s));
+    NormArgs na{};
+    na.x = d_x; na.h = h; na.M = Lv; na.split = Lv; na.eps = eps;
+    na.scale0 = scale; na.shift0 = shift;
+    HIPCK(ctx, launch_norm_ada(na, s));
+    HIPCK(ctx, launch_zero(y, (size_t)Lv * VID_OUT_PAD * 4, s));
+    GemmBatch b{};
+    b.nprob = 1;
+    b.p[0] = problem(h, DIM, io->vid_out_w, DIM, Lv, VID_OUT_PAD, DIM, y, VID_OUT_PAD);
+    b.p[0].bias = io->vid_out_b;
+    HIPCK(ctx, launch_gemm(EPI_RESID, b, s));
+    HIPCK(ctx, launch_unpatchify(y, VID_OUT_PAD, T, H, W, d_out, s));
+    return AWA_OK;
+}
 
 int dit_pack_mlp_weights(awa_ctx* ctx, const uint16_t* d_w_in, const uint16_t* d_w_gate, int mlp,
                          uint16_t* d_w_cat, awa_stream_t stream) {

@@ -8,6 +8,9 @@
 //              branch vector, the 12 modulation vectors of a layer.
 //   pack_mlp   interleave proj_in / proj_in_gate rows for the fused SwiGLU.
 //   gemv_f32   the timestep MLP (M = 1 linears, dit_vk.cpp:303-309).
+//   patchify / unpatchify   the DiT's input and output layouts
+//              (dit_vk.cpp:717-750); final_ada   the modulation vectors of
+//              the output layer (dit_vk.cpp:657-669).
 #include <cmath>
 
 #include "dit_internal.hpp"
@@ -98,6 +101,50 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
     }
 }
 
+// One row (t, hh, ww) of the patchified grid per workgroup: the 2x2 patch's
+// 33-channel pixels in (ph, pw, c) order (dit_vk.cpp:717-733), bf16, zeros
+// from column 132 up to kpad (the projection's K padding).
+__global__ __launch_bounds__(128) void patchify_kernel(const float* __restrict__ grid, int H, int W,
+                                                       uint16_t* __restrict__ out, int kpad) {
+    const int row = blockIdx.x;
+    const int H2 = H >> 1, W2 = W >> 1;
+    const int t = row / (H2 * W2), hh = (row / W2) % H2, ww = row % W2;
+    for (int j = threadIdx.x; j < kpad; j += 128) {
+        float v = 0.f;
+        if (j < 132) {
+            const int ph = j / 66, pw = (j / 33) & 1, c = j % 33;
+            v = grid[(((size_t)t * H + 2 * hh + ph) * W + 2 * ww + pw) * 33 + c];
+        }
+        out[(size_t)row * kpad + j] = (uint16_t)bf16_rne(v);
+    }
+}
+
+// The output layer's 64 values of row (t, hh, ww) back to the 2x2 patch's
+// 16-channel pixels, (ph, pw, c) order (dit_vk.cpp:735-750).
+__global__ __launch_bounds__(64) void unpatchify_kernel(const float* __restrict__ y, int ldy, int H,
+                                                        int W, float* __restrict__ out) {
+    const int row = blockIdx.x;
+    const int H2 = H >> 1, W2 = W >> 1;
+    const int t = row / (H2 * W2), hh = (row / W2) % H2, ww = row % W2;
+    const int j = threadIdx.x;  // 64 values
+    const int ph = j >> 5, pw = (j >> 4) & 1, c = j & 15;
+    out[(((size_t)t * H + 2 * hh + ph) * W + 2 * ww + pw) * 16 + c] = y[(size_t)row * ldy + j];
+}
+
+// Output layer modulation (dit_vk.cpp:657-669): RMSNorm(x) * w * (emb[6d+1] +
+// ada_scale) + (emb[6d] + ada_shift), as the scale w * (emb[6d+1] + ada_scale)
+// and the shift of norm_ada.
+__global__ __launch_bounds__(256) void final_ada_kernel(const float* __restrict__ emb,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ ada_scale,
+                                                        const float* __restrict__ ada_shift,
+                                                        float* __restrict__ scale, float* __restrict__ shift) {
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= DIM) return;
+    scale[d] = w[d] * (emb[6 * d + 1] + ada_scale[d]);
+    shift[d] = emb[6 * d] + ada_shift[d];
+}
+
 struct Sinusoid {
     float v[256];
 };
@@ -129,6 +176,27 @@ hipError_t launch_pack_mlp(const uint16_t* w_in, const uint16_t* w_gate, int mlp
 hipError_t launch_gemv_f32(const float* W, const float* b, const float* x, float* y, int in, int out,
                            int silu, hipStream_t s) {
     hipLaunchKernelGGL(gemv_f32_kernel, dim3((out + 3) / 4), dim3(256), 0, s, W, b, x, y, in, out, silu);
+    return hipGetLastError();
+}
+
+hipError_t launch_patchify(const float* grid, int T, int H, int W, uint16_t* out, int kpad, hipStream_t s) {
+    const int rows = T * (H / 2) * (W / 2);
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(patchify_kernel, dim3(rows), dim3(128), 0, s, grid, H, W, out, kpad);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpatchify(const float* y, int ldy, int T, int H, int W, float* out, hipStream_t s) {
+    const int rows = T * (H / 2) * (W / 2);
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(unpatchify_kernel, dim3(rows), dim3(64), 0, s, y, ldy, H, W, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_final_ada(const float* emb, const float* w, const float* ada_scale, const float* ada_shift,
+                            float* scale, float* shift, hipStream_t s) {
+    hipLaunchKernelGGL(final_ada_kernel, dim3((DIM + 255) / 256), dim3(256), 0, s, emb, w, ada_scale,
+                       ada_shift, scale, shift);
     return hipGetLastError();
 }
 

@@ -60,4 +60,12 @@ hipError_t launch_gemv_f32(const float* W, const float* b, const float* x, float
                            int silu, hipStream_t s);
 hipError_t launch_sinusoid(float t, float* e, int dim, hipStream_t s);
 
+// grid (T, H, W, 33) fp32 -> [T (H/2) (W/2)][kpad] bf16 patches, (ph, pw, c) order
+hipError_t launch_patchify(const float* grid, int T, int H, int W, uint16_t* out, int kpad, hipStream_t s);
+// [T (H/2) (W/2)][ldy] fp32 (first 64 columns) -> (T, H, W, 16) fp32
+hipError_t launch_unpatchify(const float* y, int ldy, int T, int H, int W, float* out, hipStream_t s);
+// output-layer modulation vectors: scale = w (emb[6d+1] + ada_scale), shift = emb[6d] + ada_shift
+hipError_t launch_final_ada(const float* emb, const float* w, const float* ada_scale, const float* ada_shift,
+                            float* scale, float* shift, hipStream_t s);
+
 }  // namespace awa

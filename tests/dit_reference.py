@@ -91,3 +91,52 @@ def to_device(br, mlp, ctx, dev):
     for k in ("nq", "nk", "attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate"):
         d[k] = f32(br[k])
     return d
+
+
+# ---- input and output layers (DitVk::forward_grid, dit_vk.cpp:752-763) ----
+
+def patchify(grid):
+    """dit_vk.cpp:717-733: (T, H, W, C) -> (T (H/2) (W/2), 4 C), patch order (ph, pw, c)."""
+    T, H, W, Cc = grid.shape
+    g = grid.reshape(T, H // 2, 2, W // 2, 2, Cc)          # t, hh, ph, ww, pw, c
+    return np.ascontiguousarray(g.transpose(0, 1, 3, 2, 4, 5).reshape(-1, 4 * Cc))
+
+
+def unpatchify(y, T, H, W, Cc=16):
+    """dit_vk.cpp:735-750: (T (H/2) (W/2), 4 C) -> (T, H, W, C)."""
+    g = y.reshape(T, H // 2, W // 2, 2, 2, Cc)              # t, hh, ww, ph, pw, c
+    return np.ascontiguousarray(g.transpose(0, 1, 3, 2, 4, 5).reshape(T, H, W, Cc))
+
+
+def random_io(rng, O=None, scale=0.02):
+    """Input/output layer weights ~ N(0, 0.02) (bf16-representable if O is given)."""
+    r = (lambda a: O.bf16_round(a)) if O is not None else (lambda a: a)
+    f = lambda *s: (scale * rng.standard_normal(s)).astype(np.float32)
+    return {"vid_in_w": r(f(DIM, 132)), "vid_in_b": f(DIM), "txt_in_w": r(f(DIM, 5120)), "txt_in_b": f(DIM),
+            "out_norm_w": (1 + f(DIM)).astype(np.float32), "out_ada_shift": f(DIM),
+            "out_ada_scale": f(DIM), "vid_out_w": r(f(64, DIM)), "vid_out_b": f(64)}
+
+
+def io_to_device(io, dev):
+    import torch
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, torch.bfloat16)
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, torch.float32)
+    return {k: (bf(v) if k.endswith("_w") and k != "out_norm_w" else f32(v)) for k, v in io.items()}
+
+
+def embed_emulation(O, grid, txt, io, bf16=True):
+    """forward_latent's input projections (dit_vk.cpp:494-497) on the patchified grid;
+    with bf16=True the projection inputs are rounded to bf16 as the block stores them."""
+    rnd = O.bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
+    xv = rnd(patchify(grid)) @ io["vid_in_w"].T + io["vid_in_b"]
+    xt = rnd(txt) @ io["txt_in_w"].T + io["txt_in_b"]
+    return np.concatenate([xv, xt]).astype(np.float32)
+
+
+def final_emulation(O, x_vid, emb, io, T, H, W, eps=1e-5, bf16=True):
+    """forward_latent's output layer (dit_vk.cpp:657-675) and unpatchify (:735-750)."""
+    rnd = O.bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
+    vn = rmsnorm_rows(x_vid, eps) * io["out_norm_w"]
+    h = rnd(vn * (emb[1::6] + io["out_ada_scale"]) + (emb[0::6] + io["out_ada_shift"]))
+    y = h @ io["vid_out_w"].T + io["vid_out_b"]
+    return unpatchify(y.astype(np.float32), T, H, W)

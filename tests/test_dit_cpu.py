@@ -42,3 +42,46 @@ def test_last_layer_text_skips_mlp(oracle):
         b = layer_emulation(oracle, x, emb, vb2, vb2, g, g.Lv, TXT, last=last, bf16=False)
         assert not np.array_equal(a[: g.Lv], b[: g.Lv])
         assert np.array_equal(a[g.Lv:], b[g.Lv:]) == last
+
+
+def test_patchify_known_answer():
+    """Row (t, hh, ww), column (ph*2 + pw)*33 + c holds grid[t, 2hh+ph, 2ww+pw, c]
+    (dit_vk.cpp:717-733), on a grid whose values encode their own indices."""
+    from dit_reference import patchify
+    T, H, W, Cc = 2, 6, 8, 33
+    t, h, w, c = np.meshgrid(np.arange(T), np.arange(H), np.arange(W), np.arange(Cc), indexing="ij")
+    grid = (t * 1000000 + h * 10000 + w * 100 + c).astype(np.float32)
+    p = patchify(grid)
+    assert p.shape == (T * (H // 2) * (W // 2), 132)
+    for row in (0, 5, 11, 23):
+        tt, rem = divmod(row, (H // 2) * (W // 2))
+        hh, ww = divmod(rem, W // 2)
+        for j in (0, 32, 33, 65, 66, 100, 131):
+            ph, pw, cc = j // 66, (j // 33) % 2, j % 33
+            assert p[row, j] == tt * 1000000 + (2 * hh + ph) * 10000 + (2 * ww + pw) * 100 + cc
+
+
+def test_unpatchify_inverts_patchify():
+    """dit_vk.cpp:735-750 writes back exactly the (ph, pw, c) order that
+    patchify reads, so the two are inverse on a 16-channel grid."""
+    from dit_reference import patchify, unpatchify
+    rng = np.random.default_rng(7)
+    g = rng.standard_normal((2, 10, 14, 16)).astype(np.float32)
+    assert np.array_equal(unpatchify(patchify(g), 2, 10, 14), g)
+
+
+def test_final_emulation_matches_oracle(oracle):
+    """The output layer in fp32 against the oracle's rmsnorm (with weight) and
+    linear (dit_vk.cpp:657-675), row by row."""
+    from dit_reference import final_emulation, random_emb, random_io, unpatchify
+    rng = np.random.default_rng(8)
+    io = random_io(rng)
+    emb, _ = random_emb(rng, oracle)
+    T, H, W = 1, 4, 6
+    Lv = T * (H // 2) * (W // 2)
+    x = rng.standard_normal((Lv, 2560)).astype(np.float32)
+    got = final_emulation(oracle, x, emb, io, T, H, W, bf16=False)
+    vn = np.stack([oracle.rmsnorm(x[i], io["out_norm_w"]) for i in range(Lv)])
+    vn = vn * (emb[1::6] + io["out_ada_scale"]) + (emb[0::6] + io["out_ada_shift"])
+    ref = unpatchify(oracle.linear(vn, io["vid_out_w"], io["vid_out_b"]), T, H, W)
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-5), np.abs(got - ref).max()

@@ -103,3 +103,80 @@ def test_layer_1080p(oracle, ctx, kind):
         dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
         note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
         assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
+
+
+def test_embed_and_final(oracle, ctx):
+    """dit_embed / dit_final (input projections and the output layer) against
+    their emulation at the block's bf16 rounding points."""
+    import torch
+    from dit_reference import embed_emulation, final_emulation, io_to_device, random_io
+    note("embed / final")
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(60)
+    T, H, W, TXT = 2, 24, 40, 9
+    io = random_io(rng, oracle)
+    grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
+    txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
+    emb, _ = random_emb(rng, oracle)
+    dio = ctx.io_layers(io_to_device(io, dev))
+    x = ctx.embed(dio, torch.from_numpy(grid).to(dev), torch.from_numpy(txt).to(dev))
+    torch.cuda.synchronize()
+    ref = embed_emulation(oracle, grid, txt, io)
+    cos, rel, _ = metrics(x.cpu().numpy(), ref)
+    note(f"  embed cos={cos:.8f} rel={rel:.2e}")
+    assert cos >= 0.99999 and rel <= 1e-3, (cos, rel)
+    out = ctx.final(dio, torch.from_numpy(emb).to(dev), x, T, H, W)
+    torch.cuda.synchronize()
+    Lv = T * (H // 2) * (W // 2)
+    ref_out = final_emulation(oracle, x.cpu().numpy()[:Lv], emb, io, T, H, W)
+    cos, rel, _ = metrics(out.cpu().numpy(), ref_out)
+    note(f"  final cos={cos:.8f} rel={rel:.2e}")
+    assert out.shape == (T, H, W, 16)
+    assert cos >= BF16_COS, (cos, rel)
+
+
+def test_embed_rejects_odd_grid(ctx, awa):
+    import torch
+    from dit_reference import io_to_device, random_io
+    rng = np.random.default_rng(61)
+    dio = ctx.io_layers(io_to_device(random_io(rng), torch.device("cuda:0")))
+    grid = torch.zeros((1, 5, 8, 33), device="cuda:0")
+    txt = torch.zeros((4, 5120), device="cuda:0")
+    x = torch.empty((2 * 4 + 4, 2560), device="cuda:0")
+    with pytest.raises(awa.AwaError):
+        ctx.embed(dio, grid, txt, x=x)
+
+
+def test_forward_grid_two_layers(oracle, ctx):
+    """forward_grid (dit_vk.cpp:752-763) with two layers (unshifted, then shifted
+    geometry, dual branches on the first): grid in, 16-channel grid out."""
+    import torch
+    from dit_reference import embed_emulation, final_emulation, io_to_device, random_io
+    note("forward_grid 2 layers")
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(62)
+    T, H, W, TXT, mlp, nw = 1, 24, 40, 9, 256, (4, 3, 3)
+    io = random_io(rng, oracle)
+    grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
+    txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
+    emb, _ = random_emb(rng, oracle)
+    b0v, b0t, b1 = (random_branch(rng, mlp, oracle) for _ in range(3))
+    g = [oracle.Geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    Lv = g[0].Lv
+    x = embed_emulation(oracle, grid, txt, io)
+    x = layer_emulation(oracle, x, emb, b0v, b0t, g[0], Lv, TXT)
+    x = layer_emulation(oracle, x, emb, b1, b1, g[1], Lv, TXT)
+    ref = final_emulation(oracle, x[:Lv], emb, io, T, H, W)
+
+    dio = ctx.io_layers(io_to_device(io, dev))
+    geoms = [ctx.build_geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    d0v, d0t, d1 = (to_device(b, mlp, ctx, dev) for b in (b0v, b0t, b1))
+    demb = torch.from_numpy(emb).to(dev)
+    dx = ctx.embed(dio, torch.from_numpy(grid).to(dev), torch.from_numpy(txt).to(dev))
+    ctx.layer(geoms[0], d0v, d0t, demb, dx, Lv, TXT, mlp=mlp)
+    ctx.layer(geoms[1], d1, d1, demb, dx, Lv, TXT, mlp=mlp)
+    out = ctx.final(dio, demb, dx, T, H, W)
+    torch.cuda.synchronize()
+    cos, rel, _ = metrics(out.cpu().numpy(), ref)
+    note(f"  out cos={cos:.8f} rel={rel:.2e}")
+    assert cos >= BF16_COS, (cos, rel)
