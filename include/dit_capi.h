@@ -121,6 +121,30 @@ int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H,
 int dit_final(awa_ctx* ctx, const dit_io* io, const float* d_emb, const float* d_x, int T, int H,
               int W, float eps, float* d_out, awa_stream_t stream);
 
+/* Timestep MLP weights of dit_time_embedding (fp32, [out][in]). */
+typedef struct {
+    const float* w_in;   /* [2560][256]   */
+    const float* b_in;   /* [2560]        */
+    const float* w_hid;  /* [2560][2560]  */
+    const float* b_hid;  /* [2560]        */
+    const float* w_out;  /* [15360][2560] */
+    const float* b_out;  /* [15360]       */
+} dit_time_weights;
+
+/* The whole DiT, DitVk::forward_grid (dit_vk.cpp:752-763) with
+ * forward_latent(0, n_layers, init, final) (dit_vk.cpp:486-691): dit_embed,
+ * the timestep embedding at t, n_layers x dit_layer_forward (layer i with
+ * branches vb[i] / tb[i], geometry g_even on even i and g_odd on odd i,
+ * dit_vk.cpp:518; the last layer with txt_vid_only = last_txt_vid_only),
+ * then dit_final into d_out fp32 (T, H, W, 16).  The geometries are built
+ * on the latent grid (T, H/2, W/2) with TXT text rows.  d_x is the caller's
+ * residual stream, fp32 [Lv + TXT][2560]; the embedding lives in the context. */
+int dit_forward_grid(awa_ctx* ctx, const dit_io* io, const dit_time_weights* tw,
+                     const dit_branch* const* vb, const dit_branch* const* tb, int n_layers,
+                     const awa_geom* g_even, const awa_geom* g_odd, int mlp, int last_txt_vid_only,
+                     float eps, float t, const float* d_grid, int T, int H, int W, const float* d_txt,
+                     int TXT, float* d_x, float* d_out, awa_stream_t stream);
+
 /* Plain bf16 GEMM with the block's kernel, for tests and measurement:
  * C[M][N] = A[M][K] W[N][K]^T, bf16 in, bf16 out (fp32 accumulation).
  * N a multiple of 256, K a multiple of 64. */

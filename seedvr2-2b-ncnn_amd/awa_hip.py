@@ -47,6 +47,11 @@ class DitIoWeights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in IO_FIELDS]
 
 
+class DitTimeWeights(C.Structure):
+    """dit_time_weights of include/dit_capi.h (device pointers)."""
+    _fields_ = [(n, C.c_void_p) for n in ("w_in", "b_in", "w_hid", "b_hid", "w_out", "b_out")]
+
+
 class GeomInfo(C.Structure):
     _fields_ = [(n, C.c_int32) for n in
                 ("t", "h", "w", "nwin", "sumf", "Lv", "txt_len", "max_S", "n_tiles", "n_items")]
@@ -103,6 +108,10 @@ def lib():
         L.dit_io_destroy.restype = None
         L.dit_embed.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, vp]
         L.dit_final.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, vp]
+        L.dit_forward_grid.argtypes = [vp, vp, C.POINTER(DitTimeWeights), C.POINTER(C.POINTER(DitBranch)),
+                                       C.POINTER(C.POINTER(DitBranch)), C.c_int, vp, vp, C.c_int, C.c_int,
+                                       C.c_float, C.c_float, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp,
+                                       vp, vp]
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
@@ -308,6 +317,37 @@ class Context:
         rc = lib().dit_final(self.ptr, io.ptr, C.c_void_p(emb.data_ptr()), C.c_void_p(x.data_ptr()), int(T),
                              int(H), int(W), float(eps), C.c_void_p(out.data_ptr()), _stream_ptr(stream))
         self.check(rc, "dit_final")
+        return out
+
+    def forward_grid(self, io, time_w, layers, geom_even, geom_odd, t, grid, txt, mlp=6912,
+                     last_txt_vid_only=False, eps=1e-5, x=None, out=None, stream=None):
+        """dit_forward_grid.  time_w: 6 device tensors (w_in, b_in, w_hid, b_hid, w_out, b_out);
+        layers: list of (video branch dict, text branch dict) of device tensors."""
+        import torch
+        T, H, W, _ = grid.shape
+        TXT = txt.shape[0]
+        Lv = T * (H // 2) * (W // 2)
+        if x is None:
+            x = torch.empty((Lv + TXT, DIM), dtype=torch.float32, device=grid.device)
+        if out is None:
+            out = torch.empty((T, H, W, 16), dtype=torch.float32, device=grid.device)
+        tw = DitTimeWeights(*[w.data_ptr() for w in time_w])
+        cache = {}
+
+        def br(d):
+            if id(d) not in cache:
+                cache[id(d)] = DitBranch(**{k: d[k].data_ptr() for k in BRANCH_FIELDS})
+            return cache[id(d)]
+        n = len(layers)
+        vb = (C.POINTER(DitBranch) * max(n, 1))(*[C.pointer(br(v)) for v, _ in layers])
+        tb = (C.POINTER(DitBranch) * max(n, 1))(*[C.pointer(br(t_)) for _, t_ in layers])
+        rc = lib().dit_forward_grid(self.ptr, io.ptr, C.byref(tw), vb, tb, n, geom_even.ptr,
+                                    geom_odd.ptr if geom_odd is not None else None, int(mlp),
+                                    int(bool(last_txt_vid_only)), float(eps), float(t),
+                                    C.c_void_p(grid.data_ptr()), int(T), int(H), int(W),
+                                    C.c_void_p(txt.data_ptr()), int(TXT), C.c_void_p(x.data_ptr()),
+                                    C.c_void_p(out.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_forward_grid")
         return out
 
     def dit_timing_read(self):

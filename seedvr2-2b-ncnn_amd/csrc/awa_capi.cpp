@@ -349,6 +349,7 @@ void awa_destroy(awa_ctx* ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->small) (void)hipFree(ctx->small);
+    if (ctx->emb) (void)hipFree(ctx->emb);
     for (hipEvent_t e : ctx->ev_free) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->ev_used) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->dit_ev_used) (void)hipEventDestroy(e);

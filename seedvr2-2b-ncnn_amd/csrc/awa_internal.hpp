@@ -131,6 +131,7 @@ struct awa_ctx {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     float* small = nullptr;
+    float* emb = nullptr;  // dit_forward_grid: the timestep embedding [15360]
 };
 
 struct awa_geom {

@@ -340,6 +340,41 @@ int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb, con
     return AWA_OK;
 }
 
+int dit_forward_grid(awa_ctx* ctx, const dit_io* io, const dit_time_weights* tw, const dit_branch* const* vb,
+                     const dit_branch* const* tb, int n_layers, const awa_geom* g_even, const awa_geom* g_odd,
+                     int mlp, int last_txt_vid_only, float eps, float t, const float* d_grid, int T, int H,
+                     int W, const float* d_txt, int TXT, float* d_x, float* d_out, awa_stream_t stream) {
+    if (!ctx || !io || !tw || !vb || !tb || n_layers < 0 || !g_even || (n_layers > 1 && !g_odd)) {
+        set_err(ctx, "dit_forward_grid: null argument or n_layers=%d < 0", n_layers);
+        return AWA_EARG;
+    }
+    if (H % 2 || W % 2 || H < 2 || W < 2 || T < 1) {
+        set_err(ctx, "dit_forward_grid: T=%d H=%d W=%d (H and W even)", T, H, W);
+        return AWA_EARG;
+    }
+    const int Lv = T * (H / 2) * (W / 2);
+    for (const awa_geom* g : {g_even, g_odd}) {
+        if (g && (g->plan.Lv != Lv || g->plan.txt_len != TXT)) {
+            set_err(ctx, "dit_forward_grid: geometry (Lv=%d TXT=%d) does not match the grid (Lv=%d TXT=%d)",
+                    g->plan.Lv, g->plan.txt_len, Lv, TXT);
+            return AWA_EARG;
+        }
+    }
+    {
+        DeviceGuard dg(ctx->device);
+        if (!ctx->emb) HIPCK(ctx, hipMalloc(reinterpret_cast<void**>(&ctx->emb), DIT_EMB * sizeof(float)));
+    }
+    int rc = dit_embed(ctx, io, d_grid, T, H, W, d_txt, TXT, d_x, stream);
+    if (rc == AWA_OK)
+        rc = dit_time_embedding(ctx, t, tw->w_in, tw->b_in, tw->w_hid, tw->b_hid, tw->w_out, tw->b_out, ctx->emb,
+                                stream);
+    for (int i = 0; i < n_layers && rc == AWA_OK; i++)
+        rc = dit_layer_forward(ctx, (i % 2 == 0) ? g_even : g_odd, vb[i], tb[i], ctx->emb, mlp,
+                               (i == n_layers - 1) ? last_txt_vid_only : 0, eps, d_x, Lv, TXT, stream);
+    if (rc == AWA_OK) rc = dit_final(ctx, io, ctx->emb, d_x, T, H, W, eps, d_out, stream);
+    return rc;
+}
+
 int dit_timing_read(awa_ctx* ctx, double* ms_gemm, double* ms_awa, double* ms_eltwise, int* layers) {
     if (!ctx) return AWA_EARG;
     DeviceGuard dg(ctx->device);

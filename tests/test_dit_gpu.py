@@ -180,3 +180,38 @@ def test_forward_grid_two_layers(oracle, ctx):
     cos, rel, _ = metrics(out.cpu().numpy(), ref)
     note(f"  out cos={cos:.8f} rel={rel:.2e}")
     assert cos >= BF16_COS, (cos, rel)
+
+
+def test_forward_grid_call(oracle, ctx):
+    """dit_forward_grid in one call (embed, timestep MLP, three layers with the
+    last one text-free as forward_latent's, final) against the emulation chain."""
+    import torch
+    from dit_reference import embed_emulation, final_emulation, io_to_device, random_io
+    note("dit_forward_grid 3 layers")
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(63)
+    T, H, W, TXT, mlp, nw = 1, 24, 40, 9, 256, (4, 3, 3)
+    io = random_io(rng, oracle)
+    grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
+    txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
+    emb, tws = random_emb(rng, oracle)   # time_embedding(1000) of these weights
+    br = [random_branch(rng, mlp, oracle) for _ in range(4)]
+    layers = [(br[0], br[1]), (br[2], br[2]), (br[3], br[3])]
+    g = [oracle.Geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    Lv = g[0].Lv
+    x = embed_emulation(oracle, grid, txt, io)
+    for i, (vb, tb) in enumerate(layers):
+        x = layer_emulation(oracle, x, emb, vb, tb, g[i % 2], Lv, TXT, last=(i == len(layers) - 1))
+    ref = final_emulation(oracle, x[:Lv], emb, io, T, H, W)
+
+    dio = ctx.io_layers(io_to_device(io, dev))
+    geoms = [ctx.build_geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    dbr = [to_device(b, mlp, ctx, dev) for b in br]
+    dl = [(dbr[0], dbr[1]), (dbr[2], dbr[2]), (dbr[3], dbr[3])]
+    dtw = [torch.from_numpy(w).to(dev) for w in tws]
+    out = ctx.forward_grid(dio, dtw, dl, geoms[0], geoms[1], 1000.0, torch.from_numpy(grid).to(dev),
+                           torch.from_numpy(txt).to(dev), mlp=mlp, last_txt_vid_only=True)
+    torch.cuda.synchronize()
+    cos, rel, _ = metrics(out.cpu().numpy(), ref)
+    note(f"  out cos={cos:.8f} rel={rel:.2e}")
+    assert cos >= BF16_COS, (cos, rel)
