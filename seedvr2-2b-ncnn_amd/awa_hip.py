@@ -108,6 +108,21 @@ def lib():
         L.dit_io_destroy.restype = None
         L.dit_embed.argtypes = [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, vp]
         L.dit_final.argtypes = [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, vp]
+        L.dit_host_last_error.restype = C.c_char_p
+        L.dit_free_host.argtypes = [vp]
+        L.dit_free_host.restype = None
+        L.dit_read_raw_f.argtypes = [C.c_char_p, C.POINTER(vp), C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                     C.POINTER(C.c_int)]
+        L.dit_read_linear.argtypes = [C.c_char_p, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int),
+                                      C.POINTER(C.c_int)]
+        L.dit_read_win.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int64), C.POINTER(vp), C.POINTER(vp),
+                                   C.POINTER(C.c_int64), C.POINTER(vp), C.POINTER(C.c_int64)]
+        L.dit_model_load.argtypes = [vp, C.c_char_p, C.c_int, C.c_int, C.POINTER(vp), vp]
+        L.dit_model_info.argtypes = [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.dit_model_forward_grid.argtypes = [vp, vp, vp, vp, C.c_int, C.c_float, C.c_float, vp, C.c_int, C.c_int,
+                                             C.c_int, vp, C.c_int, vp, vp, vp]
+        L.dit_model_destroy.argtypes = [vp, vp]
+        L.dit_model_destroy.restype = None
         L.dit_forward_grid.argtypes = [vp, vp, C.POINTER(DitTimeWeights), C.POINTER(C.POINTER(DitBranch)),
                                        C.POINTER(C.POINTER(DitBranch)), C.c_int, vp, vp, C.c_int, C.c_int,
                                        C.c_float, C.c_float, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp,
@@ -116,6 +131,52 @@ def lib():
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
     return _lib
+
+
+def _host_array(ptr, n, dtype):
+    """Copy n values from a dit_* host buffer, then free it."""
+    ct = {np.float32: C.c_float, np.int32: C.c_int32}[dtype]
+    a = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ct)), shape=(int(n),)).copy() if n else np.zeros(0, dtype)
+    lib().dit_free_host(ptr)
+    return a
+
+
+class HostError(RuntimeError):
+    pass
+
+
+def _host_check(rc, what):
+    if rc != 0:
+        raise HostError(f"{what}: {lib().dit_host_last_error().decode()}")
+
+
+def read_raw_f(path):
+    """dit_read_raw_f: the array with its stored shape."""
+    p, n, nd = C.c_void_p(), C.c_int64(), C.c_int()
+    shape = (C.c_int64 * 8)()
+    _host_check(lib().dit_read_raw_f(str(path).encode(), C.byref(p), C.byref(n), shape, C.byref(nd)), "dit_read_raw_f")
+    return _host_array(p, n.value, np.float32).reshape([shape[i] for i in range(nd.value)])
+
+
+def read_linear(base, has_bias):
+    """dit_read_linear: (W [out][in] float32, bias or None)."""
+    w, b, no, ni = C.c_void_p(), C.c_void_p(), C.c_int(), C.c_int()
+    _host_check(lib().dit_read_linear(str(base).encode(), int(bool(has_bias)), C.byref(w), C.byref(b),
+                                      C.byref(no), C.byref(ni)), "dit_read_linear")
+    W = _host_array(w, no.value * ni.value, np.float32).reshape(no.value, ni.value)
+    return W, (_host_array(b, no.value, np.float32) if has_bias else None)
+
+
+def read_win(path, txt_len):
+    """dit_read_win: dict with header, slices [nwin][6], vid_freq, txt_freq."""
+    hdr = (C.c_int64 * 10)()
+    sl, vf, tf = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    nv, nt = C.c_int64(), C.c_int64()
+    _host_check(lib().dit_read_win(str(path).encode(), int(txt_len), hdr, C.byref(sl), C.byref(vf), C.byref(nv),
+                                   C.byref(tf), C.byref(nt)), "dit_read_win")
+    nwin = hdr[9]
+    return {"header": list(hdr), "slices": _host_array(sl, 6 * nwin, np.int32).reshape(nwin, 6),
+            "vid_freq": _host_array(vf, nv.value, np.float32), "txt_freq": _host_array(tf, nt.value, np.float32)}
 
 
 def header_symbols():
@@ -350,6 +411,32 @@ class Context:
         self.check(rc, "dit_forward_grid")
         return out
 
+    def load_model(self, path, n_layers, mm_layers, stream=None):
+        """dit_model_load of a model directory in the reference's layout."""
+        h = C.c_void_p()
+        self.check(lib().dit_model_load(self.ptr, str(path).encode(), int(n_layers), int(mm_layers), C.byref(h),
+                                        _stream_ptr(stream)), "dit_model_load")
+        return DitModel(self, h)
+
+    def model_forward_grid(self, model, geom_even, geom_odd, t, grid, txt, last_txt_vid_only=False, eps=1e-5,
+                           x=None, out=None, stream=None):
+        import torch
+        T, H, W, _ = grid.shape
+        TXT = txt.shape[0]
+        Lv = T * (H // 2) * (W // 2)
+        if x is None:
+            x = torch.empty((Lv + TXT, DIM), dtype=torch.float32, device=grid.device)
+        if out is None:
+            out = torch.empty((T, H, W, 16), dtype=torch.float32, device=grid.device)
+        rc = lib().dit_model_forward_grid(self.ptr, model.ptr, geom_even.ptr,
+                                          geom_odd.ptr if geom_odd is not None else None,
+                                          int(bool(last_txt_vid_only)), float(eps), float(t),
+                                          C.c_void_p(grid.data_ptr()), int(T), int(H), int(W),
+                                          C.c_void_p(txt.data_ptr()), int(TXT), C.c_void_p(x.data_ptr()),
+                                          C.c_void_p(out.data_ptr()), _stream_ptr(stream))
+        self.check(rc, "dit_model_forward_grid")
+        return out
+
     def dit_timing_read(self):
         a, b, c = C.c_double(), C.c_double(), C.c_double()
         n = C.c_int()
@@ -416,6 +503,29 @@ class DitIo:
     def close(self):
         if self.ptr:
             lib().dit_io_destroy(self.ctx.ptr, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DitModel:
+    """Handle of dit_model_load; destroyed with the object."""
+
+    def __init__(self, ctx, ptr):
+        self.ctx, self.ptr = ctx, ptr
+
+    def info(self):
+        a, b, c = C.c_int(), C.c_int(), C.c_int()
+        lib().dit_model_info(self.ptr, C.byref(a), C.byref(b), C.byref(c))
+        return {"n_layers": a.value, "mm_layers": b.value, "mlp": c.value}
+
+    def close(self):
+        if self.ptr:
+            lib().dit_model_destroy(self.ctx.ptr, self.ptr)
             self.ptr = None
 
     def __del__(self):

@@ -1,0 +1,414 @@
+// dit_model.cpp — readers of the reference's on-disk formats (read_raw_f,
+// ncnn InnerProduct .param/.bin, window files) and the loader of a model
+// directory in its layout onto the device.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "dit_internal.hpp"
+#include "dit_model.h"
+
+using namespace awa;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return -1;
+}
+
+// IEEE 754 binary16 -> binary32 (exact): sign, 5-bit exponent (bias 15),
+// 10-bit fraction; exponent 0: subnormal (fraction x 2^-24), 31: inf / NaN.
+float half_to_float(uint16_t h) {
+    const int e = (h >> 10) & 31, m = h & 1023;
+    float v;
+    if (e == 0) v = std::ldexp((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = std::ldexp((float)(m | 1024), e - 25);
+    return (h & 0x8000) ? -v : v;
+}
+
+bool file_size(std::ifstream& f, int64_t* n) {
+    f.seekg(0, std::ios::end);
+    *n = (int64_t)f.tellg();
+    f.seekg(0, std::ios::beg);
+    return *n >= 0;
+}
+
+constexpr uint32_t TAG_FP16 = 0x01306B47u;  // ncnn weight storage tags
+constexpr uint32_t TAG_FP32 = 0u;
+
+// One InnerProduct layer: weights [n_out][n_in] and optional bias, on the host.
+struct HostLinear {
+    std::vector<float> w, b;
+    int n_out = 0, n_in = 0;
+};
+
+int read_linear_host(const std::string& base, bool has_bias, HostLinear& L) {
+    std::ifstream pf(base + ".param");
+    if (!pf) return fail("cannot open %s.param", base.c_str());
+    std::string line;
+    long numout = -1, total = -1;
+    while (std::getline(pf, line)) {
+        std::istringstream ss(line);
+        std::string type;
+        if (!(ss >> type) || type != "InnerProduct") continue;
+        std::string tok;
+        while (ss >> tok) {
+            if (tok.rfind("0=", 0) == 0) numout = std::strtol(tok.c_str() + 2, nullptr, 10);
+            if (tok.rfind("2=", 0) == 0) total = std::strtol(tok.c_str() + 2, nullptr, 10);
+        }
+        break;
+    }
+    if (numout <= 0 || total <= 0 || total % numout)
+        return fail("%s.param: no InnerProduct line with 0=num_output and 2=weight_data_size", base.c_str());
+    L.n_out = (int)numout;
+    L.n_in = (int)(total / numout);
+    std::ifstream bf(base + ".bin", std::ios::binary);
+    if (!bf) return fail("cannot open %s.bin", base.c_str());
+    int64_t size;
+    file_size(bf, &size);
+    uint32_t tag = 0;
+    bf.read(reinterpret_cast<char*>(&tag), 4);
+    const int64_t n = total;
+    const int64_t wbytes = tag == TAG_FP16 ? 2 * n : 4 * n;
+    if (tag != TAG_FP16 && tag != TAG_FP32) return fail("%s.bin: unsupported weight storage tag 0x%08x", base.c_str(), tag);
+    if (size < 4 + wbytes + (has_bias ? 4 * numout : 0))
+        return fail("%s.bin: %lld bytes, short of the %ld x %ld weight%s", base.c_str(), (long long)size, numout,
+                    total / numout, has_bias ? " and bias" : "");
+    L.w.resize(n);
+    if (tag == TAG_FP16) {
+        std::vector<uint16_t> hw(n);
+        bf.read(reinterpret_cast<char*>(hw.data()), 2 * n);
+        for (int64_t i = 0; i < n; i++) L.w[i] = half_to_float(hw[i]);
+    } else {
+        bf.read(reinterpret_cast<char*>(L.w.data()), 4 * n);
+    }
+    if (has_bias) {
+        L.b.resize(numout);
+        bf.read(reinterpret_cast<char*>(L.b.data()), 4 * numout);
+    }
+    if (!bf) return fail("%s.bin: read error", base.c_str());
+    return 0;
+}
+
+int read_raw_host(const std::string& path, std::vector<float>& data, std::vector<int64_t>& shape) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return fail("cannot open %s", path.c_str());
+    int64_t size;
+    file_size(f, &size);
+    int64_t nd = -1;
+    f.read(reinterpret_cast<char*>(&nd), 8);
+    if (!f || nd < 0 || nd > 8) return fail("%s: bad ndim %lld", path.c_str(), (long long)nd);
+    shape.resize(nd);
+    int64_t total = 1;
+    for (auto& d : shape) {
+        f.read(reinterpret_cast<char*>(&d), 8);
+        if (!f || d < 0 || (d > 0 && total > ((int64_t)1 << 40) / d)) return fail("%s: bad shape", path.c_str());
+        total *= d;
+    }
+    if (size < 8 + 8 * nd + 4 * total)
+        return fail("%s: %lld bytes, short of %lld floats", path.c_str(), (long long)size, (long long)total);
+    data.resize(total);
+    f.read(reinterpret_cast<char*>(data.data()), 4 * total);
+    if (!f) return fail("%s: read error", path.c_str());
+    return 0;
+}
+
+template <typename T>
+T* copy_out(const std::vector<T>& v) {
+    T* p = static_cast<T*>(std::malloc(v.empty() ? 1 : v.size() * sizeof(T)));
+    if (p && !v.empty()) std::memcpy(p, v.data(), v.size() * sizeof(T));
+    return p;
+}
+
+}  // namespace
+
+struct dit_model {
+    int device = 0;
+    int n_layers = 0, mm_layers = 0, mlp = 0;
+    std::vector<void*> allocs;       // every device buffer of the model
+    std::vector<dit_branch> vb, tb;  // per layer (tb[i] == vb[i] for shared layers)
+    dit_io* io = nullptr;
+    dit_time_weights tw{};
+};
+
+extern "C" {
+
+const char* dit_host_last_error(void) { return g_err.c_str(); }
+void dit_free_host(void* p) { std::free(p); }
+
+int dit_read_raw_f(const char* path, float** data, int64_t* count, int64_t shape[8], int* ndim) {
+    if (!path || !data || !count) return fail("dit_read_raw_f: null argument");
+    std::vector<float> d;
+    std::vector<int64_t> sh;
+    if (read_raw_host(path, d, sh)) return -1;
+    *data = copy_out(d);
+    *count = (int64_t)d.size();
+    if (ndim) *ndim = (int)sh.size();
+    if (shape)
+        for (size_t i = 0; i < sh.size(); i++) shape[i] = sh[i];
+    return 0;
+}
+
+int dit_read_linear(const char* base, int has_bias, float** w, float** b, int* n_out, int* n_in) {
+    if (!base || !w) return fail("dit_read_linear: null argument");
+    HostLinear L;
+    if (read_linear_host(base, has_bias != 0, L)) return -1;
+    *w = copy_out(L.w);
+    if (b) *b = has_bias ? copy_out(L.b) : nullptr;
+    if (n_out) *n_out = L.n_out;
+    if (n_in) *n_in = L.n_in;
+    return 0;
+}
+
+int dit_read_win(const char* path, int txt_len, int64_t header[10], int32_t** slices, float** vid_freq,
+                 int64_t* n_vid, float** txt_freq, int64_t* n_txt) {
+    if (!path || !header || !slices || !vid_freq || !txt_freq || txt_len < 0)
+        return fail("dit_read_win: bad argument");
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return fail("cannot open %s", path);
+    int64_t size;
+    file_size(f, &size);
+    f.read(reinterpret_cast<char*>(header), 80);
+    const int64_t nwin = header[9];
+    if (!f || nwin < 1 || nwin > 4096) return fail("%s: bad header (nwin %lld)", path, (long long)nwin);
+    std::vector<int64_t> sl(nwin * 6);
+    f.read(reinterpret_cast<char*>(sl.data()), nwin * 48);
+    const int64_t nf = (size - 80 - nwin * 48) / 4;
+    const int64_t nt = nwin * txt_len * 126;
+    if (!f || nf < nt || (nf - nt) % 126)
+        return fail("%s: %lld floats do not split into vid_freq and %lld txt_freq floats", path, (long long)nf,
+                    (long long)nt);
+    std::vector<float> all(nf);
+    f.read(reinterpret_cast<char*>(all.data()), nf * 4);
+    if (!f) return fail("%s: read error", path);
+    std::vector<int32_t> s32(sl.begin(), sl.end());
+    *slices = copy_out(s32);
+    *vid_freq = copy_out(std::vector<float>(all.begin(), all.end() - nt));
+    *txt_freq = copy_out(std::vector<float>(all.end() - nt, all.end()));
+    if (n_vid) *n_vid = nf - nt;
+    if (n_txt) *n_txt = nt;
+    return 0;
+}
+
+void dit_model_destroy(awa_ctx* ctx, dit_model* m) {
+    if (!m) return;
+    DeviceGuard dg(ctx ? ctx->device : m->device);
+    if (m->io) dit_io_destroy(ctx, m->io);
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+int dit_model_load(awa_ctx* ctx, const char* dir, int n_layers, int mm_layers, dit_model** out,
+                   awa_stream_t stream) {
+    if (!ctx || !dir || !out || n_layers < 0 || mm_layers < 0 || mm_layers > n_layers) {
+        set_err(ctx, "dit_model_load: bad argument (n_layers=%d mm_layers=%d)", n_layers, mm_layers);
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    std::string root(dir);
+    if (!root.empty() && root.back() != '/') root += '/';
+    dit_model* m = new dit_model();
+    m->device = ctx->device;
+    m->n_layers = n_layers;
+    m->mm_layers = mm_layers;
+    float* stage = nullptr;  // fp32 staging of one matrix on its way to bf16
+    size_t stage_n = 0;
+    int rc = AWA_OK;
+
+    auto bad = [&](const char* fmt, const char* a, long x, long y) {
+        set_err(ctx, fmt, a, x, y);
+        rc = AWA_EARG;
+    };
+    auto dev_alloc = [&](size_t bytes) -> void* {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            set_err(ctx, "dit_model_load: hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+            rc = AWA_EHIP;
+            return nullptr;
+        }
+        m->allocs.push_back(p);
+        return p;
+    };
+    auto upload_f32 = [&](const std::vector<float>& v) -> float* {
+        float* p = static_cast<float*>(dev_alloc(v.size() * 4));
+        if (!p) return nullptr;
+        hipError_t e = hipMemcpy(p, v.data(), v.size() * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            set_err(ctx, "dit_model_load: %s", hipGetErrorString(e));
+            rc = AWA_EHIP;
+            return nullptr;
+        }
+        return p;
+    };
+    auto upload_bf16 = [&](const std::vector<float>& v) -> uint16_t* {
+        if (stage_n < v.size()) {
+            if (stage) (void)hipFree(stage);
+            stage = nullptr;
+            stage_n = 0;
+            if (hipMalloc(reinterpret_cast<void**>(&stage), v.size() * 4) != hipSuccess) {
+                set_err(ctx, "dit_model_load: hipMalloc of the staging buffer failed");
+                rc = AWA_EHIP;
+                return nullptr;
+            }
+            stage_n = v.size();
+        }
+        uint16_t* p = static_cast<uint16_t*>(dev_alloc(v.size() * 2));
+        if (!p) return nullptr;
+        hipError_t e = hipMemcpy(stage, v.data(), v.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = launch_cast_f32_bf16(stage, p, (int64_t)v.size(), s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);  // the staging buffer is reused
+        if (e != hipSuccess) {
+            set_err(ctx, "dit_model_load: %s", hipGetErrorString(e));
+            rc = AWA_EHIP;
+            return nullptr;
+        }
+        return p;
+    };
+    auto linear = [&](const std::string& name, bool bias, int n_out, int n_in, HostLinear& L) {
+        if (rc != AWA_OK) return false;
+        if (read_linear_host(root + name, bias, L)) {
+            set_err(ctx, "dit_model_load: %s", g_err.c_str());
+            rc = AWA_EARG;
+            return false;
+        }
+        if ((n_out > 0 && L.n_out != n_out) || (n_in > 0 && L.n_in != n_in)) {
+            bad("dit_model_load: %s is %ld x %ld", name.c_str(), L.n_out, L.n_in);
+            return false;
+        }
+        return true;
+    };
+    auto vec = [&](const std::string& name, size_t n) -> float* {
+        if (rc != AWA_OK) return nullptr;
+        std::vector<float> v;
+        std::vector<int64_t> sh;
+        if (read_raw_host(root + name + ".bin", v, sh)) {
+            set_err(ctx, "dit_model_load: %s", g_err.c_str());
+            rc = AWA_EARG;
+            return nullptr;
+        }
+        if (v.size() != n) {
+            bad("dit_model_load: %s.bin holds %ld floats, expected %ld", name.c_str(), (long)v.size(), (long)n);
+            return nullptr;
+        }
+        return upload_f32(v);
+    };
+
+    // input / output layers and the timestep MLP
+    HostLinear L;
+    dit_io_weights iw{};
+    if (linear("vid_in_proj", true, DIM, 132, L)) { iw.vid_in_w = upload_bf16(L.w); iw.vid_in_b = upload_f32(L.b); }
+    if (linear("txt_in", true, DIM, 5120, L)) { iw.txt_in_w = upload_bf16(L.w); iw.txt_in_b = upload_f32(L.b); }
+    if (linear("vid_out_proj", true, 64, DIM, L)) { iw.vid_out_w = upload_bf16(L.w); iw.vid_out_b = upload_f32(L.b); }
+    iw.out_norm_w = vec("vid_out_norm_w", DIM);
+    iw.out_ada_shift = vec("vid_out_ada_shift", DIM);
+    iw.out_ada_scale = vec("vid_out_ada_scale", DIM);
+    if (linear("emb_proj_in", true, DIM, 256, L)) { m->tw.w_in = upload_f32(L.w); m->tw.b_in = upload_f32(L.b); }
+    if (linear("emb_proj_hid", true, DIM, DIM, L)) { m->tw.w_hid = upload_f32(L.w); m->tw.b_hid = upload_f32(L.b); }
+    if (linear("emb_proj_out", true, DIT_EMB, DIM, L)) { m->tw.w_out = upload_f32(L.w); m->tw.b_out = upload_f32(L.b); }
+    if (rc == AWA_OK) rc = dit_io_create(ctx, &iw, &m->io, stream);
+
+    // layers: dual branches below mm_layers, one shared branch above
+    auto branch = [&](const std::string& b, dit_branch& br) {
+        HostLinear qkv, o, mi, mg, mo;
+        if (linear(b + "_qkv", false, QKV, DIM, qkv)) br.qkv_w = upload_bf16(qkv.w);
+        if (linear(b + "_out", true, DIM, DIM, o)) { br.out_w = upload_bf16(o.w); br.out_b = upload_f32(o.b); }
+        if (linear(b + "_mlp_in", false, m->mlp > 0 ? m->mlp : 0, DIM, mi) &&
+            linear(b + "_mlp_g", false, mi.n_out, DIM, mg) && linear(b + "_mlp_out", false, DIM, mi.n_out, mo)) {
+            if (mi.n_out % 128) {
+                bad("dit_model_load: %s MLP width %ld (%ld) is not a multiple of 128", b.c_str(), mi.n_out, 0);
+            } else {
+                m->mlp = mi.n_out;
+                uint16_t* win = upload_bf16(mi.w);
+                uint16_t* wg = upload_bf16(mg.w);
+                uint16_t* cat = static_cast<uint16_t*>(dev_alloc((size_t)2 * m->mlp * DIM * 2));
+                if (rc == AWA_OK && win && wg && cat) {
+                    hipError_t e = launch_pack_mlp(win, wg, m->mlp, cat, s);
+                    if (e != hipSuccess) {
+                        set_err(ctx, "dit_model_load: %s", hipGetErrorString(e));
+                        rc = AWA_EHIP;
+                    }
+                }
+                br.mlp_w = cat;
+                br.mlp_out_w = upload_bf16(mo.w);
+            }
+        }
+        br.nq = vec(b + "_nq", 128);
+        br.nk = vec(b + "_nk", 128);
+        br.attn_shift = vec(b + "_attn_shift", DIM);
+        br.attn_scale = vec(b + "_attn_scale", DIM);
+        br.attn_gate = vec(b + "_attn_gate", DIM);
+        br.mlp_shift = vec(b + "_mlp_shift", DIM);
+        br.mlp_scale = vec(b + "_mlp_scale", DIM);
+        br.mlp_gate = vec(b + "_mlp_gate", DIM);
+    };
+    m->vb.resize(n_layers);
+    m->tb.resize(n_layers);
+    for (int i = 0; i < n_layers && rc == AWA_OK; i++) {
+        const std::string p = "b" + std::to_string(i);
+        if (i < mm_layers) {
+            branch(p + "_vid", m->vb[i]);
+            branch(p + "_txt", m->tb[i]);
+        } else {
+            branch(p + "_all", m->vb[i]);
+            m->tb[i] = m->vb[i];
+        }
+    }
+    if (rc == AWA_OK) {
+        hipError_t e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            set_err(ctx, "dit_model_load: %s", hipGetErrorString(e));
+            rc = AWA_EHIP;
+        }
+    }
+    if (stage) (void)hipFree(stage);
+    if (rc != AWA_OK) {
+        dit_model_destroy(ctx, m);
+        return rc;
+    }
+    *out = m;
+    return AWA_OK;
+}
+
+int dit_model_info(const dit_model* m, int* n_layers, int* mm_layers, int* mlp) {
+    if (!m) return AWA_EARG;
+    if (n_layers) *n_layers = m->n_layers;
+    if (mm_layers) *mm_layers = m->mm_layers;
+    if (mlp) *mlp = m->mlp;
+    return AWA_OK;
+}
+
+int dit_model_forward_grid(awa_ctx* ctx, const dit_model* m, const awa_geom* g_even, const awa_geom* g_odd,
+                           int last_txt_vid_only, float eps, float t, const float* d_grid, int T, int H, int W,
+                           const float* d_txt, int TXT, float* d_x, float* d_out, awa_stream_t stream) {
+    if (!ctx || !m) {
+        set_err(ctx, "dit_model_forward_grid: null argument");
+        return AWA_EARG;
+    }
+    std::vector<const dit_branch*> vb(m->n_layers), tb(m->n_layers);
+    for (int i = 0; i < m->n_layers; i++) {
+        vb[i] = &m->vb[i];
+        tb[i] = (i < m->mm_layers) ? &m->tb[i] : &m->vb[i];  // shared layers: the same branch
+    }
+    return dit_forward_grid(ctx, m->io, &m->tw, vb.data(), tb.data(), m->n_layers, g_even, g_odd, m->mlp,
+                            last_txt_vid_only, eps, t, d_grid, T, H, W, d_txt, TXT, d_x, d_out, stream);
+}
+
+}  // extern "C"

@@ -215,3 +215,53 @@ def test_forward_grid_call(oracle, ctx):
     cos, rel, _ = metrics(out.cpu().numpy(), ref)
     note(f"  out cos={cos:.8f} rel={rel:.2e}")
     assert cos >= BF16_COS, (cos, rel)
+
+
+def test_model_directory(oracle, ctx, tmp_path):
+    """A model directory in the reference's layout (fp16 InnerProduct weights,
+    read_raw_f vectors; two layers, the first dual) through dit_model_load and
+    dit_model_forward_grid, against the emulation on the weights as stored."""
+    import torch
+    from dit_reference import embed_emulation, final_emulation, random_io
+    from model_files import write_model
+    note("model directory")
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(64)
+    T, H, W, TXT, mlp, nw, t = 1, 24, 40, 9, 256, (4, 3, 3), 500.0
+    io = random_io(rng)
+    br = [random_branch(rng, mlp) for _ in range(3)]
+    layers = [(br[0], br[1]), (br[2], br[2])]
+    _, tws = random_emb(rng, oracle)
+    write_model(str(tmp_path), io, layers, tws, mm_layers=1)
+    # the weights as the loader holds them: fp16 on disk, bf16 on the device (the
+    # timestep MLP stays fp32)
+    h = lambda a: a.astype(np.float16).astype(np.float32)
+    hb = lambda a: oracle.bf16_round(h(a))
+    io_d = {k: (hb(v) if k in ("vid_in_w", "txt_in_w", "vid_out_w") else v) for k, v in io.items()}
+    lin = ("qkv_w", "out_w", "mlp_in_w", "mlp_g_w", "mlp_out_w")
+    br_d = [{k: (hb(v) if k in lin else v) for k, v in b.items()} for b in br]
+    emb = oracle.time_embedding(t, *[h(w) if w.ndim == 2 else w for w in tws])
+    grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
+    txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
+    g = [oracle.Geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    Lv = g[0].Lv
+    x = embed_emulation(oracle, grid, txt, io_d)
+    x = layer_emulation(oracle, x, emb, br_d[0], br_d[1], g[0], Lv, TXT)
+    x = layer_emulation(oracle, x, emb, br_d[2], br_d[2], g[1], Lv, TXT)
+    ref = final_emulation(oracle, x[:Lv], emb, io_d, T, H, W)
+
+    model = ctx.load_model(tmp_path, 2, 1)
+    assert model.info() == {"n_layers": 2, "mm_layers": 1, "mlp": mlp}
+    geoms = [ctx.build_geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    out = ctx.model_forward_grid(model, geoms[0], geoms[1], t, torch.from_numpy(grid).to(dev),
+                                 torch.from_numpy(txt).to(dev))
+    torch.cuda.synchronize()
+    cos, rel, _ = metrics(out.cpu().numpy(), ref)
+    note(f"  out cos={cos:.8f} rel={rel:.2e}")
+    assert cos >= BF16_COS, (cos, rel)
+
+
+def test_model_directory_errors(ctx, awa, tmp_path):
+    """A missing or mis-shaped file fails the load with a message, nothing loaded."""
+    with pytest.raises(awa.AwaError, match="cannot open"):
+        ctx.load_model(tmp_path, 1, 0)
