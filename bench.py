@@ -125,12 +125,37 @@ def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912):
     ctx.timing(False)
     assert bool(torch.isfinite(x).all()), "non-finite hidden state"
     step_s = (t1 - t0) / steps
+
+    # the same step captured as one HIP graph (the launches above, recorded on a
+    # side stream) and replayed; each step starts from x0, so a replay must equal
+    # the eager result bit for bit
+    x_eager = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        one_step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        one_step()
+    x.zero_()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x, x_eager), "graph replay differs from the eager step"
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_s = (time.perf_counter() - t0) / steps
+    del graph
     M = Lv + TXT
     gemm_flops = 32 * 2 * M * 2560 * (7680 + 2560 + 3 * mlp)
     for g in geoms:
         g.close()
     return {"value": round(step_s, 5), "unit": "s per 32-layer DiT step", "steps": steps,
-            "warmup": warmup, "mlp": mlp,
+            "warmup": warmup, "mlp": mlp, "graph_replay_s": round(graph_s, 5),
             "txt_semantics": "text rows processed on every layer (merged-graph order)",
             "per_step_ms": {"gemm": round(ms_gemm / steps, 3), "awa": round(ms_awa / steps, 3),
                             "norm_ada_eltwise": round(ms_elt / steps, 3)},

@@ -69,6 +69,23 @@ int dit_model_forward_grid(awa_ctx* ctx, const dit_model* m, const awa_geom* g_e
                            float* d_x, float* d_out, awa_stream_t stream);
 void dit_model_destroy(awa_ctx* ctx, dit_model* m);
 
+/* dit_model_forward_grid captured into one HIP graph per resolution (the
+ * host orchestration of dit_graph.cpp:264-549 as a single replay).  The graph
+ * runs on a private context of its own (its scratch cannot be reallocated
+ * under it); creation runs the forward once eagerly on that context (leaving
+ * its result in d_out), then captures it.  dit_graph_launch replays the whole
+ * forward with the same arguments, reading the current contents of d_grid and
+ * d_txt.  The model, the geometries and the buffers must outlive the graph;
+ * launches of one graph must not overlap.  The capture stream must be a
+ * created stream (the null stream cannot be captured). */
+typedef struct dit_graph dit_graph;
+int dit_graph_create(awa_ctx* ctx, const dit_model* m, const awa_geom* g_even, const awa_geom* g_odd,
+                     int last_txt_vid_only, float eps, float t, const float* d_grid, int T, int H, int W,
+                     const float* d_txt, int TXT, float* d_x, float* d_out, awa_stream_t stream,
+                     dit_graph** out);
+int dit_graph_launch(awa_ctx* ctx, dit_graph* g, awa_stream_t stream);
+void dit_graph_destroy(dit_graph* g);
+
 #ifdef __cplusplus
 }
 #endif

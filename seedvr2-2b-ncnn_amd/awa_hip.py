@@ -123,6 +123,11 @@ def lib():
                                              C.c_int, vp, C.c_int, vp, vp, vp]
         L.dit_model_destroy.argtypes = [vp, vp]
         L.dit_model_destroy.restype = None
+        L.dit_graph_create.argtypes = [vp, vp, vp, vp, C.c_int, C.c_float, C.c_float, vp, C.c_int, C.c_int,
+                                       C.c_int, vp, C.c_int, vp, vp, vp, C.POINTER(vp)]
+        L.dit_graph_launch.argtypes = [vp, vp, vp]
+        L.dit_graph_destroy.argtypes = [vp]
+        L.dit_graph_destroy.restype = None
         L.dit_forward_grid.argtypes = [vp, vp, C.POINTER(DitTimeWeights), C.POINTER(C.POINTER(DitBranch)),
                                        C.POINTER(C.POINTER(DitBranch)), C.c_int, vp, vp, C.c_int, C.c_int,
                                        C.c_float, C.c_float, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp,
@@ -437,6 +442,21 @@ class Context:
         self.check(rc, "dit_model_forward_grid")
         return out
 
+    def model_graph(self, model, geom_even, geom_odd, t, grid, txt, x, out, last_txt_vid_only=False,
+                    eps=1e-5, stream=None):
+        """dit_graph_create: model_forward_grid captured for these buffers (run
+        once eagerly, so out already holds the result); DitGraph.launch replays it."""
+        T, H, W, _ = grid.shape
+        h = C.c_void_p()
+        rc = lib().dit_graph_create(self.ptr, model.ptr, geom_even.ptr,
+                                    geom_odd.ptr if geom_odd is not None else None,
+                                    int(bool(last_txt_vid_only)), float(eps), float(t),
+                                    C.c_void_p(grid.data_ptr()), int(T), int(H), int(W),
+                                    C.c_void_p(txt.data_ptr()), int(txt.shape[0]), C.c_void_p(x.data_ptr()),
+                                    C.c_void_p(out.data_ptr()), _stream_ptr(stream), C.byref(h))
+        self.check(rc, "dit_graph_create")
+        return DitGraph(self, h.value, (model, geom_even, geom_odd, grid, txt, x, out))
+
     def dit_timing_read(self):
         a, b, c = C.c_double(), C.c_double(), C.c_double()
         n = C.c_int()
@@ -503,6 +523,27 @@ class DitIo:
     def close(self):
         if self.ptr:
             lib().dit_io_destroy(self.ctx.ptr, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DitGraph:
+    """Handle of dit_graph_create; keeps what the graph reads alive."""
+
+    def __init__(self, ctx, ptr, keep):
+        self.ctx, self.ptr, self._keep = ctx, ptr, keep
+
+    def launch(self, stream=None):
+        self.ctx.check(lib().dit_graph_launch(self.ctx.ptr, self.ptr, _stream_ptr(stream)), "dit_graph_launch")
+
+    def close(self):
+        if self.ptr:
+            lib().dit_graph_destroy(self.ptr)
             self.ptr = None
 
     def __del__(self):

@@ -411,4 +411,77 @@ int dit_model_forward_grid(awa_ctx* ctx, const dit_model* m, const awa_geom* g_e
                             last_txt_vid_only, eps, t, d_grid, T, H, W, d_txt, TXT, d_x, d_out, stream);
 }
 
+struct dit_graph {
+    int device = 0;
+    awa_ctx* priv = nullptr;  // owns the scratch baked into the graph
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+void dit_graph_destroy(dit_graph* g) {
+    if (!g) return;
+    DeviceGuard dg(g->device);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    if (g->priv) awa_destroy(g->priv);
+    delete g;
+}
+
+int dit_graph_create(awa_ctx* ctx, const dit_model* m, const awa_geom* g_even, const awa_geom* g_odd,
+                     int last_txt_vid_only, float eps, float t, const float* d_grid, int T, int H, int W,
+                     const float* d_txt, int TXT, float* d_x, float* d_out, awa_stream_t stream, dit_graph** out) {
+    if (!ctx || !m || !out || !stream) {
+        set_err(ctx, "dit_graph_create: null argument (capture needs a created stream, not the null stream)");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    DeviceGuard dg(ctx->device);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    dit_graph* g = new dit_graph();
+    g->device = ctx->device;
+    int rc = awa_create(&g->priv, ctx->device);
+    if (rc != AWA_OK) {
+        set_err(ctx, "dit_graph_create: private context: %s", g->priv ? awa_last_error(g->priv) : "awa_create failed");
+        dit_graph_destroy(g);
+        return rc;
+    }
+    // eager run: sizes the private context's buffers (no allocation may happen
+    // while capturing) and checks every argument
+    rc = dit_model_forward_grid(g->priv, m, g_even, g_odd, last_txt_vid_only, eps, t, d_grid, T, H, W, d_txt, TXT,
+                                d_x, d_out, stream);
+    hipError_t e = rc == AWA_OK ? hipStreamSynchronize(s) : hipSuccess;
+    if (rc == AWA_OK && e == hipSuccess) {
+        e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            rc = dit_model_forward_grid(g->priv, m, g_even, g_odd, last_txt_vid_only, eps, t, d_grid, T, H, W,
+                                        d_txt, TXT, d_x, d_out, stream);
+            hipError_t e2 = hipStreamEndCapture(s, &g->graph);
+            if (rc == AWA_OK) e = e2;
+        }
+        if (rc == AWA_OK && e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    }
+    if (rc != AWA_OK || e != hipSuccess) {
+        if (rc != AWA_OK) set_err(ctx, "dit_graph_create: %s", awa_last_error(g->priv));
+        else set_err(ctx, "dit_graph_create: %s", hipGetErrorString(e));
+        dit_graph_destroy(g);
+        return rc != AWA_OK ? rc : AWA_EHIP;
+    }
+    *out = g;
+    return AWA_OK;
+}
+
+int dit_graph_launch(awa_ctx* ctx, dit_graph* g, awa_stream_t stream) {
+    if (!ctx || !g) {
+        set_err(ctx, "dit_graph_launch: null argument");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(g->device);
+    hipError_t e = hipGraphLaunch(g->exec, reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        set_err(ctx, "dit_graph_launch: %s", hipGetErrorString(e));
+        return AWA_EHIP;
+    }
+    return AWA_OK;
+}
+
 }  // extern "C"

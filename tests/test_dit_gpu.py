@@ -217,17 +217,34 @@ def test_forward_grid_call(oracle, ctx):
     assert cos >= BF16_COS, (cos, rel)
 
 
+SMALL_MODEL = dict(T=1, H=24, W=40, TXT=9, mlp=256, nw=(4, 3, 3), t=500.0)
+
+
+def _model_reference(oracle, io_d, br_d, emb, grid, txt):
+    """The two-layer small model (first layer dual) on the weights as the
+    loader holds them, through the layer emulation."""
+    from dit_reference import embed_emulation, final_emulation
+    T, H, W, _ = grid.shape
+    TXT, nw = txt.shape[0], SMALL_MODEL["nw"]
+    g = [oracle.Geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
+    Lv = g[0].Lv
+    x = embed_emulation(oracle, grid, txt, io_d)
+    x = layer_emulation(oracle, x, emb, br_d[0], br_d[1], g[0], Lv, TXT)
+    x = layer_emulation(oracle, x, emb, br_d[2], br_d[2], g[1], Lv, TXT)
+    return final_emulation(oracle, x[:Lv], emb, io_d, T, H, W)
+
+
 def test_model_directory(oracle, ctx, tmp_path):
     """A model directory in the reference's layout (fp16 InnerProduct weights,
     read_raw_f vectors; two layers, the first dual) through dit_model_load and
     dit_model_forward_grid, against the emulation on the weights as stored."""
     import torch
-    from dit_reference import embed_emulation, final_emulation, random_io
+    from dit_reference import random_io
     from model_files import write_model
     note("model directory")
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(64)
-    T, H, W, TXT, mlp, nw, t = 1, 24, 40, 9, 256, (4, 3, 3), 500.0
+    T, H, W, TXT, mlp, nw, t = (SMALL_MODEL[k] for k in ("T", "H", "W", "TXT", "mlp", "nw", "t"))
     io = random_io(rng)
     br = [random_branch(rng, mlp) for _ in range(3)]
     layers = [(br[0], br[1]), (br[2], br[2])]
@@ -243,12 +260,7 @@ def test_model_directory(oracle, ctx, tmp_path):
     emb = oracle.time_embedding(t, *[h(w) if w.ndim == 2 else w for w in tws])
     grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
     txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
-    g = [oracle.Geometry(T, H // 2, W // 2, nw, TXT, s) for s in (0, 1)]
-    Lv = g[0].Lv
-    x = embed_emulation(oracle, grid, txt, io_d)
-    x = layer_emulation(oracle, x, emb, br_d[0], br_d[1], g[0], Lv, TXT)
-    x = layer_emulation(oracle, x, emb, br_d[2], br_d[2], g[1], Lv, TXT)
-    ref = final_emulation(oracle, x[:Lv], emb, io_d, T, H, W)
+    ref = _model_reference(oracle, io_d, br_d, emb, grid, txt)
 
     model = ctx.load_model(tmp_path, 2, 1)
     assert model.info() == {"n_layers": 2, "mm_layers": 1, "mlp": mlp}
@@ -259,6 +271,40 @@ def test_model_directory(oracle, ctx, tmp_path):
     cos, rel, _ = metrics(out.cpu().numpy(), ref)
     note(f"  out cos={cos:.8f} rel={rel:.2e}")
     assert cos >= BF16_COS, (cos, rel)
+
+    # the same forward captured in a HIP graph, replayed on new inputs: every
+    # replay equals the eager forward bit for bit (no kernel here reduces with
+    # atomics), with eager work and synchronisations between the replays
+    note("model graph")
+    s = torch.cuda.Stream()
+    d_grid = torch.from_numpy(grid).to(dev)
+    d_txt = torch.from_numpy(txt).to(dev)
+    Lv = T * (H // 2) * (W // 2)
+    x = torch.empty((Lv + TXT, 2560), dtype=torch.float32, device=dev)
+    gout = torch.empty((T, H, W, 16), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    graph = ctx.model_graph(model, geoms[0], geoms[1], t, d_grid, d_txt, x, gout, stream=s)
+    s.synchronize()
+    assert torch.equal(gout, out), "graph creation's eager run differs from the forward"
+    for rep in range(3):
+        grid2 = rng.standard_normal((T, H, W, 33)).astype(np.float32)
+        txt2 = rng.standard_normal((TXT, 5120)).astype(np.float32)
+        d_grid.copy_(torch.from_numpy(grid2))
+        d_txt.copy_(torch.from_numpy(txt2))
+        torch.cuda.synchronize()
+        eager = ctx.model_forward_grid(model, geoms[0], geoms[1], t, d_grid, d_txt)
+        torch.cuda.synchronize()
+        gout.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.launch(stream=s)
+        s.synchronize()
+        note(f"  replay {rep}: max |graph - eager| = {(gout - eager).abs().max().item():.3e}")
+        assert torch.equal(gout, eager), rep
+        if rep == 0:
+            cos, rel, _ = metrics(gout.cpu().numpy(), _model_reference(oracle, io_d, br_d, emb, grid2, txt2))
+            note(f"  replay cos={cos:.8f} rel={rel:.2e}")
+            assert cos >= BF16_COS, (cos, rel)
+    graph.close()
 
 
 def test_model_directory_errors(ctx, awa, tmp_path):
