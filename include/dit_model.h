@@ -69,6 +69,34 @@ int dit_model_forward_grid(awa_ctx* ctx, const dit_model* m, const awa_geom* g_e
                            float* d_x, float* d_out, awa_stream_t stream);
 void dit_model_destroy(awa_ctx* ctx, dit_model* m);
 
+/* The merged whole-model graph <g>.param / <g>.bin (export_dit_graph.py:
+ * 47-258, loaded by DitVk's graph path, dit_graph.cpp:114-151): layer lines
+ * Input, AdaCompose, InnerProduct (proj_vid_in, proj_txt_in, qkv_<i>_<v|t>,
+ * out_, min_, mig_, mout_, outproj), RMSNorm (rn_fin with gamma), AWA
+ * (awa_<i>), BinaryOp, Swish; the .bin is what each layer's load_model reads,
+ * in layer order: AdaCompose's tagged vectors (per layer and flow attn_shift,
+ * attn_scale, attn_gate, mlp_shift, mlp_scale, mlp_gate; then the output
+ * layer's shift and scale, ada_compose.cpp:35-89), InnerProduct tagged weights
+ * then raw bias, AWA four tagged 128-vectors (nq_v, nk_v, nq_t, nk_t,
+ * awa_layer.cpp:38-52), the final RMSNorm's raw gamma.  Only a whole graph
+ * (with the in_vid0 input and the output layer) is a model; block subgraphs
+ * are refused.  The timestep MLP is not in the graph (the host runs it,
+ * dit_graph.cpp:270): emb_proj_in/_hid/_out come from dir, the model
+ * directory, as they do for DitVk::init.  mm_layers: the number of dual-branch
+ * layers, -1 to take it from AdaCompose's 2= (required for a graph without
+ * AdaCompose, whose ada vectors then also come from dir). */
+int dit_model_load_graph(awa_ctx* ctx, const char* param, const char* bin, const char* dir, int mm_layers,
+                         dit_model** out, awa_stream_t stream);
+/* Host checks of a merged graph: its layer count, dual-branch count and the
+ * number of distinct weights it indexes; and one weight by its model-directory
+ * name (b3_vid_qkv, b12_all_nq, vid_out_norm_w, ...): linear weights as
+ * [n_out][n_in] float32 with *b the bias or NULL, vectors with *n_out values
+ * and *n_in = 0.  0, or -1 with dit_host_last_error(). */
+int dit_graph_file_info(const char* param, const char* bin, int mm_layers, int* n_layers, int* mm_out,
+                        int* n_weights);
+int dit_read_graph_weight(const char* param, const char* bin, int mm_layers, const char* name, float** w,
+                          float** b, int* n_out, int* n_in);
+
 /* dit_model_forward_grid captured into one HIP graph per resolution (the
  * host orchestration of dit_graph.cpp:264-549 as a single replay).  The graph
  * runs on a private context of its own (its scratch cannot be reallocated

@@ -118,6 +118,11 @@ def lib():
         L.dit_read_win.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int64), C.POINTER(vp), C.POINTER(vp),
                                    C.POINTER(C.c_int64), C.POINTER(vp), C.POINTER(C.c_int64)]
         L.dit_model_load.argtypes = [vp, C.c_char_p, C.c_int, C.c_int, C.POINTER(vp), vp]
+        L.dit_model_load_graph.argtypes = [vp, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int, C.POINTER(vp), vp]
+        L.dit_graph_file_info.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                          C.POINTER(C.c_int)]
+        L.dit_read_graph_weight.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_char_p, C.POINTER(vp),
+                                            C.POINTER(vp), C.POINTER(C.c_int), C.POINTER(C.c_int)]
         L.dit_model_info.argtypes = [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]
         L.dit_model_forward_grid.argtypes = [vp, vp, vp, vp, C.c_int, C.c_float, C.c_float, vp, C.c_int, C.c_int,
                                              C.c_int, vp, C.c_int, vp, vp, vp]
@@ -182,6 +187,27 @@ def read_win(path, txt_len):
     nwin = hdr[9]
     return {"header": list(hdr), "slices": _host_array(sl, 6 * nwin, np.int32).reshape(nwin, 6),
             "vid_freq": _host_array(vf, nv.value, np.float32), "txt_freq": _host_array(tf, nt.value, np.float32)}
+
+
+def graph_file_info(param, bin_path, mm_layers=-1):
+    """dit_graph_file_info: (n_layers, mm_layers, distinct weights) of a merged graph."""
+    n, mm, nw = C.c_int(), C.c_int(), C.c_int()
+    _host_check(lib().dit_graph_file_info(str(param).encode(), str(bin_path).encode(), int(mm_layers), C.byref(n),
+                                          C.byref(mm), C.byref(nw)), "dit_graph_file_info")
+    return n.value, mm.value, nw.value
+
+
+def read_graph_weight(param, bin_path, name, mm_layers=-1):
+    """dit_read_graph_weight: (W [out][in], bias or None) of a linear weight, or
+    (vector, None), by its model-directory name."""
+    w, b, no, ni = C.c_void_p(), C.c_void_p(), C.c_int(), C.c_int()
+    _host_check(lib().dit_read_graph_weight(str(param).encode(), str(bin_path).encode(), int(mm_layers),
+                                            name.encode(), C.byref(w), C.byref(b), C.byref(no), C.byref(ni)),
+                "dit_read_graph_weight")
+    if ni.value == 0:
+        return _host_array(w, no.value, np.float32), None
+    W = _host_array(w, no.value * ni.value, np.float32).reshape(no.value, ni.value)
+    return W, (_host_array(b, no.value, np.float32) if b.value else None)
 
 
 def header_symbols():
@@ -421,6 +447,16 @@ class Context:
         h = C.c_void_p()
         self.check(lib().dit_model_load(self.ptr, str(path).encode(), int(n_layers), int(mm_layers), C.byref(h),
                                         _stream_ptr(stream)), "dit_model_load")
+        return DitModel(self, h)
+
+    def load_graph_model(self, param, bin_path, model_dir=None, mm_layers=-1, stream=None):
+        """dit_model_load_graph: a merged whole-model graph (.param/.bin), the
+        timestep MLP from model_dir."""
+        h = C.c_void_p()
+        self.check(lib().dit_model_load_graph(self.ptr, str(param).encode(), str(bin_path).encode(),
+                                              str(model_dir).encode() if model_dir is not None else None,
+                                              int(mm_layers), C.byref(h), _stream_ptr(stream)),
+                   "dit_model_load_graph")
         return DitModel(self, h)
 
     def model_forward_grid(self, model, geom_even, geom_odd, t, grid, txt, last_txt_vid_only=False, eps=1e-5,

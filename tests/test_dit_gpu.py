@@ -306,6 +306,20 @@ def test_model_directory(oracle, ctx, tmp_path):
             assert cos >= BF16_COS, (cos, rel)
     graph.close()
 
+    # the same weights merged into one graph file (export_dit_graph.py layout),
+    # the timestep MLP from the directory: the same device weights, the same output
+    note("merged graph file")
+    from model_files import write_graph
+    write_graph(str(tmp_path), tmp_path / "g.param", tmp_path / "g.bin", 2, 1)
+    gmodel = ctx.load_graph_model(tmp_path / "g.param", tmp_path / "g.bin", tmp_path)
+    assert gmodel.info() == {"n_layers": 2, "mm_layers": 1, "mlp": mlp}
+    d_grid.copy_(torch.from_numpy(grid))
+    d_txt.copy_(torch.from_numpy(txt))
+    out2 = ctx.model_forward_grid(gmodel, geoms[0], geoms[1], t, d_grid, d_txt)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
+    gmodel.close()
+
 
 def test_model_directory_errors(ctx, awa, tmp_path):
     """A missing or mis-shaped file fails the load with a message, nothing loaded."""
