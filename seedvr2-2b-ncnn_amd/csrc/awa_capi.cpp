@@ -292,6 +292,12 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
     const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
     const size_t tpart_bytes = (size_t)P.nwin * P.txt_len * DIM * 4;
+    // the bf16 kernel addresses vattn with 32-bit buffer offsets (and marks
+    // padding rows with offsets from 2^31)
+    if (dtype == AWA_BF16 && (size_t)Lv * DIM * es > 0x7fffffffu) {
+        set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 2 GiB output addressing", Lv);
+        return AWA_EARG;
+    }
     int rc = ensure_scratch(ctx, off_t + align256(tpart_bytes));
     if (rc != AWA_OK) return rc;
     char* base = static_cast<char*>(ctx->scratch);
@@ -315,7 +321,8 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
     sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
     sa.sched_start = g->d_sched_start; sa.sched_desc = g->d_sched_desc; sa.n_slots = P.n_slots;
-    sa.vattn = d_vattn; sa.tpart = reinterpret_cast<float*>(base + off_t);
+    sa.vattn = d_vattn; sa.vattn_bytes = (uint32_t)((size_t)Lv * DIM * es);
+    sa.tpart = reinterpret_cast<float*>(base + off_t);
     sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
     sa.scale_log2e = 1.0f;  // the pack kernel folded the scale into Q

@@ -209,6 +209,7 @@ struct SdpaArgs {
     const int32_t* sched_desc;
     int n_slots;
     void* vattn;
+    uint32_t vattn_bytes;  // bf16 kernel: size of vattn (buffer stores drop beyond it)
     float* tpart;          // [nwin][txt_len][2560] fp32 text partials
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles, n_items, nwin;
     float scale_log2e;     // multiplier of the scores (1 when Q carries the scale)

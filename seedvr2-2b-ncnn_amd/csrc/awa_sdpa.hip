@@ -31,7 +31,17 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Two floats -> two bf16 (round to nearest even) in one word, low half
+// first: one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
 
 // The key/query tile sequence of one window: its video tiles, then the text
 // tiles of its text set.
@@ -104,8 +114,8 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
             const float o2 = oacc[dt][4 * g + 2] * inv, o3 = oacc[dt][4 * g + 3] * inv;
             if constexpr (kBf16Out) {
                 uint2 u;
-                u.x = bf16_rne(o0) | (bf16_rne(o1) << 16);
-                u.y = bf16_rne(o2) | (bf16_rne(o3) << 16);
+                u.x = pack_bf16x2(o0, o1);
+                u.y = pack_bf16x2(o2, o3);
                 *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(dst_row) + d0) = u;
             } else {
                 *reinterpret_cast<float4*>(reinterpret_cast<float*>(dst_row) + d0) =
@@ -173,6 +183,55 @@ __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, 
 // an 8-pass MFMA).
 typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
+
+// LDS DMA of one wave's half of a K or V^T tile: eight global_load_lds_dwordx4
+// (lane i writes 16 bytes at M0 + 16 i), instruction j filling the 1 KiB at
+// LDS byte address m + 1024 j.  Issued from asm because for the builtin the
+// compiler tracks the pending LDS writes itself: it then drains vmcnt before
+// any LDS store and, since it counts them with the LDS operations, turns every
+// later LDS wait into lgkmcnt(0), so the fragment reads of the score loop and
+// the epilogue's staging round trips could no longer overlap.  The kernel
+// waits for these loads itself (vmcnt(0) and a barrier) before any wave reads
+// the tiles they fill.  M0 written by an SALU instruction needs one wait state
+// before the DMA reads it.
+// K: instruction j reads global b[j / 4] + vo[j % 4] (b1 = b0 + 16 rows).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4], uint32_t m) {
+    asm volatile(
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b1]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b1]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b1]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b1]"
+        :
+        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b0] "s"(b0), [b1] "s"(b1),
+          [m] "s"(m)
+        : "memory", "scc", "m0");
+}
+// V^T: instruction j reads global b[j / 2] + vo[j % 2] (b[k] = b0 + 16 k rows
+// of the transposed tile).  No immediate offsets: on these instructions the
+// offset moves the LDS destination as well.
+__device__ inline void dma_v8(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t b3, const uint32_t (&vo)[2],
+                              uint32_t m) {
+    asm volatile(
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b0]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b1]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b1]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b2]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b2]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b3]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b3]"
+        :
+        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [b0] "s"(b0), [b1] "s"(b1), [b2] "s"(b2), [b3] "s"(b3),
+          [m] "s"(m)
+        : "memory", "scc", "m0");
+}
+#pragma clang diagnostic pop
 
 constexpr int KT_E = TILE * HEAD_D;         // bf16 elements of a K (or V^T) tile
 constexpr float RESCALE_LOG2 = 8.f;
@@ -333,38 +392,32 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // shifted by 16 rows.  V^T: instruction i fills rows 64 wave + 8 i .. +7,
     // logical chunk (lane % 8) ^ ((row >> 1) & 7); instruction i + 2 is
     // instruction i shifted by 16 rows.
-    int koff[4], voff[2];
+    uint32_t koff[4], voff[2];  // byte offsets within the tile
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = 32 * wave + 4 * i + (lane >> 4);
-        koff[i] = row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3);
+        koff[i] = 2 * (row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3));
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int row = 64 * wave + 8 * i + (lane >> 3);
-        voff[i] = row * TILE + (((lane & 7) ^ ((row >> 1) & 7)) << 3);
+        voff[i] = 2 * (row * TILE + (((lane & 7) ^ ((row >> 1) & 7)) << 3));
     }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lptr_t)lds;
     // tile index of key tile kk of work item W
     auto tile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
         return kk < W.nvt ? W.vbase + kk : W.tbase + (kk - W.nvt);
     };
     auto dma_k = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(a.Kp) + W.h * head_stride +
-                              (size_t)tile_of(W, kk) * KT_E;
-        uint16_t* dst = lds + slot * KT_E + wave * (KT_E / 2);
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            __builtin_amdgcn_global_load_lds((gptr_t)(src + (i >> 2) * 16 * HEAD_D + koff[i & 3]),
-                                            (lptr_t)(dst + i * 512), 16, 0, 0);
+        const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) +
+                                                        W.h * head_stride + (size_t)tile_of(W, kk) * KT_E);
+        dma_k8(src, src + 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot * KT_E + wave * (KT_E / 2)));
     };
     auto dma_v = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(a.Vp) + W.h * head_stride +
-                              (size_t)tile_of(W, kk) * KT_E;
-        uint16_t* dst = lds + (3 + slot) * KT_E + wave * (KT_E / 2);
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            __builtin_amdgcn_global_load_lds((gptr_t)(src + (i >> 1) * 16 * TILE + voff[i & 1]),
-                                            (lptr_t)(dst + i * 512), 16, 0, 0);
+        const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Vp) +
+                                                        W.h * head_stride + (size_t)tile_of(W, kk) * KT_E);
+        dma_v8(src, src + 2 * 16 * TILE, src + 2 * 32 * TILE, src + 2 * 48 * TILE, voff,
+               lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2)));
     };
     // The first K tiles and V^T tile of W into ring slots kb, kb + 1 and vb.
     auto dma_first = [&](const Work& W, int kb, int vb) __attribute__((always_inline)) {
@@ -649,20 +702,33 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                             const f32x16& o = oacc[qb][dt];
                             const float iv = inv[qb];
                             uint2 u;
-                            u.x = bf16_rne(o[4 * g] * iv) | (bf16_rne(o[4 * g + 1] * iv) << 16);
-                            u.y = bf16_rne(o[4 * g + 2] * iv) | (bf16_rne(o[4 * g + 3] * iv) << 16);
+                            u.x = pack_bf16x2(o[4 * g] * iv, o[4 * g + 1] * iv);
+                            u.y = pack_bf16x2(o[4 * g + 2] * iv, o[4 * g + 3] * iv);
                             const int c = 4 * dt + g;
                             *reinterpret_cast<uint2*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3) + 4 * hb) = u;
                         }
                 }
-                uint16_t* out = reinterpret_cast<uint16_t*>(a.vattn) + (size_t)cur.h * HEAD_D + (lane & 15) * 8;
+                // all token lookups, then all row reads, then all stores: each
+                // group waits once.  Padding rows (token -1) get an offset past
+                // the buffer's end, which the buffer store drops, so no lane
+                // branches around its store.
+                const __amdgpu_buffer_rsrc_t ores =
+                    __builtin_amdgcn_make_buffer_rsrc(a.vattn, 0, a.vattn_bytes, 0x00020000);
+                const uint32_t col = 2 * ((uint32_t)cur.h * HEAD_D + (lane & 15) * 8);
+                uint32_t ofs[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int tok = __shfl(orow_cur[i >> 3], (4 * i + (lane >> 4)) & 31);
+                    ofs[i] = tok >= 0 ? (uint32_t)tok * (2 * DIM) + col : 0x80000000u;
+                }
+                u32x4 v[16];
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int row = 4 * i + (lane >> 4), c = lane & 15;
-                    const int tok = __shfl(orow_cur[i >> 3], row & 31);
-                    const uint4 v = *reinterpret_cast<const uint4*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3));
-                    if (tok >= 0) *reinterpret_cast<uint4*>(out + (size_t)tok * DIM) = v;
+                    v[i] = *reinterpret_cast<const u32x4*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3));
                 }
+#pragma unroll
+                for (int i = 0; i < 16; i++) __builtin_amdgcn_raw_buffer_store_b128(v[i], ores, ofs[i], 0, 0);
             }
         }
         kb = (kb + nk) % 3;
