@@ -231,6 +231,29 @@ __device__ inline void dma_v8(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t b3
           [m] "s"(m)
         : "memory", "scc", "m0");
 }
+// Halves of the above (four instructions, LDS from m), for spreading a tile's
+// DMA between the MFMA slots of a unit: K half h reads base b_h with vo[0..3];
+// V^T half h reads bases ba (vo[0], vo[1]) then bb (vo[0], vo[1]).
+__device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
+    asm volatile(
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b]"
+        :
+        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b] "s"(b), [m] "s"(m)
+        : "memory", "scc", "m0");
+}
+__device__ inline void dma4_v(uint64_t ba, uint64_t bb, const uint32_t (&vo)[2], uint32_t m) {
+    asm volatile(
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[ba]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[ba]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[bb]\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[bb]"
+        :
+        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [ba] "s"(ba), [bb] "s"(bb), [m] "s"(m)
+        : "memory", "scc", "m0");
+}
 #pragma clang diagnostic pop
 
 constexpr int KT_E = TILE * HEAD_D;         // bf16 elements of a K (or V^T) tile
@@ -419,6 +442,21 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         dma_v8(src, src + 2 * 16 * TILE, src + 2 * 32 * TILE, src + 2 * 48 * TILE, voff,
                lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2)));
     };
+    // Quarter q of the DMA of key tile kk (K half q for q < 2, V^T half q - 2).
+    auto dma_quarter = [&](const Work& W, int q, int kk_k, int slot_k, int kk_v, int slot_v)
+        __attribute__((always_inline)) {
+        if (q < 2) {
+            const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) +
+                                                            W.h * head_stride + (size_t)tile_of(W, kk_k) * KT_E);
+            dma4_k(src + q * 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot_k * KT_E + wave * (KT_E / 2)) + 4096 * q);
+        } else {
+            const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Vp) +
+                                                            W.h * head_stride + (size_t)tile_of(W, kk_v) * KT_E);
+            const int h = q - 2;
+            dma4_v(src + h * 2 * 32 * TILE, src + h * 2 * 32 * TILE + 2 * 16 * TILE, voff,
+                   lds_base + 2 * ((3 + slot_v) * KT_E + wave * (KT_E / 2)) + 4096 * h);
+        }
+    };
     // The first K tiles and V^T tile of W into ring slots kb, kb + 1 and vb.
     auto dma_first = [&](const Work& W, int kb, int vb) __attribute__((always_inline)) {
         dma_k(W, 0, kb);
@@ -540,7 +578,11 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         }
 
         // One unit: phases A and B as described above.
-        auto unit = [&](int u, bool has_succ) __attribute__((always_inline)) {
+        // dk / dv: the unit also issues the tile's DMA of K tile kk_k into slot
+        // sk / V^T tile kk_v into slot sv, a quarter after each fourth score
+        // slot (the MFMAs run while the DMA instructions issue).
+        auto unit = [&](int u, bool has_succ, bool dk, bool dv, int kk_k, int sk, int kk_v, int sv)
+            __attribute__((always_inline)) {
             // ---- stale-maximum rule for this unit's scores (mtc: their row max relative to m)
             if (__any(mtc[0] > RESCALE_LOG2 || mtc[1] > RESCALE_LOG2)) {
                 float alpha[2];
@@ -594,6 +636,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
                     else qk_only(snx[qb], kf[st], qf[qb][st]);
                     if (j == 3) load_vf();
+                    if ((j == 4 || j == 8) && dk) dma_quarter(cur, j / 8, kk_k, sk, kk_v, sv);
+                    if ((j == 12 || j == 16) && dv) dma_quarter(cur, 2 + (j - 12) / 4, kk_k, sk, kk_v, sv);
                 }
             } else {
                 load_vf();
@@ -648,15 +692,20 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         // the current and next score registers alternate without copies); the
         // last tile is peeled because its second unit has no successor.
         auto tile = [&](int kk, bool last) __attribute__((always_inline)) {
-            if (kk + 2 < nk) dma_k(cur, kk + 2, (kb + kk + 2) % 3);
-            if (kk + 1 < nk) dma_v(cur, kk + 1, (vb + kk + 1) & 1);
+            const bool dk = kk + 2 < nk, dv = kk + 1 < nk;
+            const int sk = (kb + kk + 2) % 3, sv = (vb + kk + 1) & 1;
             if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1);
-            if (active) unit(2 * kk, true);
+            if (active) {
+                unit(2 * kk, true, dk, dv, kk + 2, sk, kk + 1, sv);
+            } else {  // an idle wave still fills its half of the tiles
+                if (dk) dma_k(cur, kk + 2, sk);
+                if (dv) dma_v(cur, kk + 1, sv);
+            }
             // the item's last unit computes no scores: Q is dead, so the
             // next item's query tile loads during it (after the slot's last
             // item: the same tile again, unused)
             if (last) load_q(nxt);
-            if (active) unit(2 * kk + 1, !last);
+            if (active) unit(2 * kk + 1, !last, false, false, 0, 0, 0, 0);
             if (!last) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
