@@ -306,6 +306,29 @@ def test_model_directory(oracle, ctx, tmp_path):
             assert cos >= BF16_COS, (cos, rel)
     graph.close()
 
+    # the C++ DitVk mirror (csrc/dit_vk.hpp) on the same directory and inputs:
+    # the same device path, so the same bits as the forward driven from here
+    # (with the last layer's text rows attending to video only, as
+    # forward_latent runs them)
+    note("C++ DitVk")
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "bin", "test_dit_vk")
+    assert os.path.exists(exe), f"{exe} missing: build it with make -C seedvr2-2b-ncnn_amd tests"
+    grid.tofile(tmp_path / "grid.f32")
+    txt.tofile(tmp_path / "txt.f32")
+    r = subprocess.run([exe, str(tmp_path), "2", "1", str(tmp_path / "grid.f32"), str(tmp_path / "txt.f32"),
+                        str(T), str(H), str(W), str(TXT), repr(float(t)), str(tmp_path / "out.f32")],
+                       capture_output=True, text=True, timeout=120)
+    note("  " + (r.stdout + r.stderr).strip().replace("\n", "\n  "))
+    assert r.returncode == 0, r.stderr
+    cpp_out = np.fromfile(tmp_path / "out.f32", np.float32).reshape(T, H, W, 16)
+    d_grid.copy_(torch.from_numpy(grid))
+    d_txt.copy_(torch.from_numpy(txt))
+    py_out = ctx.model_forward_grid(model, geoms[0], geoms[1], t, d_grid, d_txt, last_txt_vid_only=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(cpp_out, py_out.cpu().numpy())
+
     # the same weights merged into one graph file (export_dit_graph.py layout),
     # the timestep MLP from the directory: the same device weights, the same output
     note("merged graph file")
