@@ -191,7 +191,13 @@ def main():
         for _ in range(4):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"calibration_copy_bytes": n * 4, "launches": 4}))
+        t0 = time.perf_counter()
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 10
+        print(json.dumps({"calibration_copy_bytes": n * 4, "launches": 14,
+                          "copy_GBs_read_plus_write": round(2 * n * 4 / dt / 1e9, 1)}))
         return
 
     import awa_hip
