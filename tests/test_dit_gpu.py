@@ -345,6 +345,13 @@ def test_model_directory(oracle, ctx, tmp_path):
 
 
 def test_model_directory_errors(ctx, awa, tmp_path):
-    """A missing or mis-shaped file fails the load with a message, nothing loaded."""
+    """A missing or mis-shaped file fails the load with a message, nothing loaded;
+    a graph cannot be captured on the null stream."""
+    import ctypes as C
     with pytest.raises(awa.AwaError, match="cannot open"):
         ctx.load_model(tmp_path, 1, 0)
+    h = C.c_void_p()
+    rc = awa.lib().dit_graph_create(ctx.ptr, C.c_void_p(1), None, None, 0, 1e-5, 1000.0, None, 1, 2, 2, None, 1,
+                                    None, None, None, C.byref(h))
+    assert rc != 0 and h.value is None
+    assert "null stream" in awa.lib().awa_last_error(ctx.ptr).decode()
