@@ -123,14 +123,13 @@ void plan_tiles(GeomPlan& P) {
     P.n_items = (int)P.items.size() / 4;
 }
 
-// Static schedule of the persistent bf16 attention kernel over n_slots
-// resident workgroups.  A work item costs about its window's key-tile count
-// plus one tile for the prologue (Q load, first DMA).  All items of one
-// (window, head) go to one XCD so that they share that window's K/V tiles
-// through the XCD's L2; groups are spread over the XCDs longest first onto
-// the least loaded XCD, then each XCD's items are packed onto its slots (the
-// tighter of longest-first and a capacity-bisected first-fit-decreasing).
-// Slot s is workgroup s, dispatched to XCD s % 8.
+// Static longest-processing-time schedule of the persistent bf16 attention
+// kernel over n_slots resident workgroups.  A work item costs about its
+// window's key-tile count plus one tile for the prologue (Q load, first DMA).
+// All items of one (window, head) go to one XCD so that they share that
+// window's K/V tiles through the XCD's L2; groups are spread over the XCDs
+// longest first onto the least loaded XCD, then each XCD's items onto its
+// slots the same way.  Slot s is workgroup s, dispatched to XCD s % 8.
 void plan_schedule(GeomPlan& P, int n_slots) {
     constexpr int XCDS = 8;
     n_slots = std::max(XCDS, n_slots - n_slots % XCDS);
@@ -156,46 +155,15 @@ void plan_schedule(GeomPlan& P, int n_slots) {
     std::vector<std::vector<int>> slot_work(n_slots);
     for (int x = 0; x < XCDS; x++) {
         auto& wl = xwork[x];
-        auto cost = [&](int id) -> long { return win_cost[P.items[4 * (id % P.n_items)]]; };
-        std::stable_sort(wl.begin(), wl.end(), [&](int a, int b) { return cost(a) > cost(b); });
-        // Longest first onto the least loaded slot gives a first bound on the
-        // XCD's makespan; first-fit-decreasing into slots of capacity C, with
-        // C bisected between the load bound and that makespan, often packs the
-        // 2-3 items per slot tighter.  The better of the two is kept.
-        std::vector<int> lpt_slot(wl.size()), ffd_slot(wl.size()), best_ffd;
+        std::stable_sort(wl.begin(), wl.end(), [&](int a, int b) {
+            return win_cost[P.items[4 * (a % P.n_items)]] > win_cost[P.items[4 * (b % P.n_items)]];
+        });
         std::vector<long> sload(per_xcd, 0);
-        long total = 0, biggest = 0;
-        for (size_t i = 0; i < wl.size(); i++) {
+        for (int id : wl) {
             const int k = (int)(std::min_element(sload.begin(), sload.end()) - sload.begin());
-            sload[k] += cost(wl[i]);
-            lpt_slot[i] = k;
-            total += cost(wl[i]);
-            biggest = std::max(biggest, cost(wl[i]));
+            sload[k] += win_cost[P.items[4 * (id % P.n_items)]];
+            slot_work[x + XCDS * k].push_back(id);
         }
-        const long lpt_span = wl.empty() ? 0 : *std::max_element(sload.begin(), sload.end());
-        auto ffd_fits = [&](long cap) {
-            std::fill(sload.begin(), sload.end(), 0);
-            for (size_t i = 0; i < wl.size(); i++) {
-                int k = 0;
-                while (k < per_xcd && sload[k] + cost(wl[i]) > cap) k++;
-                if (k == per_xcd) return false;
-                sload[k] += cost(wl[i]);
-                ffd_slot[i] = k;
-            }
-            return true;
-        };
-        long lo = std::max(biggest, (total + per_xcd - 1) / per_xcd) - 1, hi = lpt_span;
-        while (hi - lo > 1) {  // invariant: cap lo fails (or is below the bounds), cap hi is LPT's or fits
-            const long mid = (lo + hi) / 2;
-            if (ffd_fits(mid)) {
-                hi = mid;
-                best_ffd = ffd_slot;
-            } else {
-                lo = mid;
-            }
-        }
-        const std::vector<int>& pick = best_ffd.empty() ? lpt_slot : best_ffd;
-        for (size_t i = 0; i < wl.size(); i++) slot_work[x + XCDS * pick[i]].push_back(wl[i]);
     }
     P.sched_start.assign(n_slots + 1, 0);
     P.sched_desc.clear();
