@@ -27,6 +27,9 @@ CONFIGS = {
     "cfg1_720p": ((1, 45, 53), (4, 3, 3), 58, 1, 0.0),
     "cfg2_1080p": ((1, 68, 80), (4, 3, 3), 58, 2, 0.0),
     "cfg4_ragged": ((1, 71, 97), (1, 4, 4), 77, 4, 0.01),
+    # several latent frames: temporal RoPE positions and windows across frames
+    "cfg5_frames": ((5, 23, 27), (4, 3, 3), 58, 5, 0.0),
+    "cfg6_frames": ((9, 8, 10), (2, 2, 3), 30, 6, 0.0),
 }
 
 
@@ -102,13 +105,32 @@ def test_f32_config0_360p(oracle, ctx, shifted):
         assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
 
 
+@pytest.mark.parametrize("name", ["cfg5_frames", "cfg6_frames"])
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_f32_multi_frame(oracle, ctx, name, shifted):
+    """fp32 path on grids of several latent frames (T > 1)."""
+    torch, _ = torch_dev()
+    grid, nw, txt, seed, _ = CONFIGS[name]
+    note(f"f32 {name} shifted={shifted}")
+    vq, tq, gains = seeded_awa_inputs(grid[0] * grid[1] * grid[2], txt, seed)
+    o = oracle.Geometry(*grid, nw, txt, shifted)
+    assert len(set(o.slices[:, 0].tolist())) > 1  # windows start on more than one frame
+    rv, rt = oracle.awa_forward(vq, tq, o, *gains, eps=1e-5)
+    geom = ctx.build_geometry(*grid, nw, txt, shifted)
+    va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.float32)
+    for out, ref in ((va, rv), (ta, rt)):
+        cos, rel, _ = metrics(out, ref)
+        note(f"  cos={cos:.8f} rel={rel:.2e}")
+        assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
 def bf16_reference(oracle, vq, tq, gains, geom_o):
     """The reference bf16 path: bf16 in, fp32 attention, bf16 out."""
     rv, rt = oracle.awa_forward(oracle.bf16_round(vq), oracle.bf16_round(tq), geom_o, *gains, eps=1e-5)
     return oracle.bf16_round(rv), oracle.bf16_round(rt)
 
 
-@pytest.mark.parametrize("name", ["cfg1_720p", "cfg2_1080p", "cfg4_ragged", "cfg0_360p"])
+@pytest.mark.parametrize("name", ["cfg1_720p", "cfg2_1080p", "cfg4_ragged", "cfg0_360p", "cfg5_frames", "cfg6_frames"])
 @pytest.mark.parametrize("shifted", [0, 1])
 def test_bf16_configs(oracle, ctx, name, shifted):
     torch, _ = torch_dev()
