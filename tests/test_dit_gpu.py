@@ -182,15 +182,17 @@ def test_forward_grid_two_layers(oracle, ctx):
     assert cos >= BF16_COS, (cos, rel)
 
 
-def test_forward_grid_call(oracle, ctx):
+@pytest.mark.parametrize("thw", [(1, 24, 40), (3, 16, 22)])
+def test_forward_grid_call(oracle, ctx, thw):
     """dit_forward_grid in one call (embed, timestep MLP, three layers with the
-    last one text-free as forward_latent's, final) against the emulation chain."""
+    last one text-free as forward_latent's, final) against the emulation chain,
+    on one latent frame and on three."""
     import torch
     from dit_reference import embed_emulation, final_emulation, io_to_device, random_io
-    note("dit_forward_grid 3 layers")
+    note(f"dit_forward_grid 3 layers {thw}")
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(63)
-    T, H, W, TXT, mlp, nw = 1, 24, 40, 9, 256, (4, 3, 3)
+    (T, H, W), TXT, mlp, nw = thw, 9, 256, (4, 3, 3)
     io = random_io(rng, oracle)
     grid = rng.standard_normal((T, H, W, 33)).astype(np.float32)
     txt = rng.standard_normal((TXT, 5120)).astype(np.float32)
