@@ -350,19 +350,23 @@ __device__ inline void acc_scale(f32x16& acc, float alpha) {
             : "v"(alpha));
     }
 }
-// acc = 0 inside asm.
+// acc = 0 inside asm: eight MFMAs with zero operands and a zero accumulator
+// (one issue slot each, where 128 v_accvgpr_write stall the item start).  The
+// leading s_nop covers the wait states between a VALU write of the zero
+// operand and its read by the MFMA.  The first readers of these registers are
+// unit 1's P.V MFMAs and, after unit 0's score MFMAs and their explicit waits,
+// the VALU (rescale, epilogue), so the 8-pass latency needs no wait of its own.
 __device__ inline void acc_zero(f32x16 (&o)[2][4]) {
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r += 4)
-                asm volatile(
-                    "v_accvgpr_write_b32 %0, 0\n\tv_accvgpr_write_b32 %1, 0\n\t"
-                    "v_accvgpr_write_b32 %2, 0\n\tv_accvgpr_write_b32 %3, 0"
-                    : "=a"(o[qb][dt][r]), "=a"(o[qb][dt][r + 1]), "=a"(o[qb][dt][r + 2]),
-                      "=a"(o[qb][dt][r + 3]));
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    asm volatile(
+        "s_nop 4\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %8, %8, 0\n\tv_mfma_f32_32x32x16_bf16 %1, %8, %8, 0\n\t"
+        "v_mfma_f32_32x32x16_bf16 %2, %8, %8, 0\n\tv_mfma_f32_32x32x16_bf16 %3, %8, %8, 0\n\t"
+        "v_mfma_f32_32x32x16_bf16 %4, %8, %8, 0\n\tv_mfma_f32_32x32x16_bf16 %5, %8, %8, 0\n\t"
+        "v_mfma_f32_32x32x16_bf16 %6, %8, %8, 0\n\tv_mfma_f32_32x32x16_bf16 %7, %8, %8, 0"
+        : "=a"(o[0][0]), "=a"(o[0][1]), "=a"(o[0][2]), "=a"(o[0][3]), "=a"(o[1][0]), "=a"(o[1][1]),
+          "=a"(o[1][2]), "=a"(o[1][3])
+        : "v"(z));
 }
 
 // Keys of a 32-key unit at or beyond kvalid get -inf.  Register r holds key
