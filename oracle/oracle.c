@@ -25,11 +25,25 @@
  *   orc_awa_forward    bit-exact against verify_dit.cpp::awa_forward compiled
  *                      into oracle/_ref (identity out-projection); fp64 SDPA
  *                      special case (one window = plain attention).
- *   orc_f32_to_bf16    table of hand-checked cases (ties to even, carries into
- *                      the exponent, signed zero).
- *   orc_dit_layer      composed of the functions above in dit_vk.cpp:517-632
- *                      order; bit-exact against the same loop written over
- *                      the reference's own functions in oracle/_ref.
+ *   orc_f32_to_bf16    a table of cases worked out by hand from the rounding
+ *                      rule (ties to even, carry into the exponent, signed
+ *                      zero, subnormals, overflow) and torch's float32 ->
+ *                      bfloat16 cast on every finite float32 pattern
+ *                      (tests/test_bf16_boundary.py); orc_bf16_to_f32 on all
+ *                      65536 patterns.
+ *   orc_dit_layer      with txt_vid_only = 0: 32 chained layers (10 dual, 22
+ *                      shared, even/odd geometry), with the input layers, the
+ *                      time embedding and the output layer around them, give
+ *                      max|diff| == 0 after blocks 0-3, 15, 31 and at the
+ *                      output against the reference's own verify_dit main()
+ *                      (verify_dit.cpp:350-485) run unchanged from oracle/_ref
+ *                      on the same model directory
+ *                      (test_dit_stack_matches_reference_main).  With
+ *                      txt_vid_only = 1 (forward_latent's last layer,
+ *                      dit_vk.cpp:523-620, which no compilable reference file
+ *                      contains): pinned by reading plus the invariant that
+ *                      the MLP weights leave the text rows untouched
+ *                      (test_last_layer_text_skips_mlp).
  *   orc_time_embedding bit-exact against verify_dit.cpp::time_embedding.
  */
 #include "oracle.h"

@@ -81,6 +81,10 @@ def ref():
         R.ref_silu.argtypes = [_f32p, C.c_int]
         R.ref_linear.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_int, C.c_int, _f32p]
         R.ref_time_embedding.argtypes = [C.c_float] + [_f32p] * 7
+        _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+        R.ref_verify_dit_main.restype = C.c_int
+        R.ref_verify_dit_main.argtypes = [C.c_char_p, _i32p, _f64p, _f64p, C.c_int,
+                                          C.POINTER(C.c_int)]
         R.ref_awa_block.argtypes = [_f32p, C.c_int, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
                                     _i32p, C.c_int, _f32p, C.c_int, _f32p, _f32p, _f32p,
                                     _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]

@@ -6,12 +6,62 @@
 // Built by oracle/Makefile into oracle/_ref/ only when the reference sources
 // are present; nothing in the product links it.
 //
-// verify_dit.cpp's main() is renamed so this file can provide the library.
+// verify_dit.cpp's main() is renamed so this file can provide the library,
+// and its fprintf calls go through report_fprintf below, which prints them as
+// before and also keeps the numbers of the per-block and final comparison
+// lines at full precision (the printed %.5f would hide a difference below
+// 5e-6).  The standard headers come first so that only the reference's own
+// code sees the macro.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <string>
+#include <vector>
+#include <unistd.h>
+
+namespace {
+struct Report {
+    int block;        // layer index, or -1 for the final vid_out line
+    double cos;
+    double maxdiff;
+};
+std::vector<Report> g_reports;
+
+int report_fprintf(FILE* f, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    va_list cp;
+    va_copy(cp, ap);
+    if (std::strncmp(fmt, "[block %d]", 10) == 0) {
+        Report r;
+        r.block = va_arg(cp, int);
+        r.cos = va_arg(cp, double);
+        r.maxdiff = va_arg(cp, double);
+        g_reports.push_back(r);
+    } else if (std::strncmp(fmt, "[FINAL vid_out]", 15) == 0) {
+        Report r;
+        r.block = -1;
+        r.cos = va_arg(cp, double);
+        r.maxdiff = va_arg(cp, double);
+        g_reports.push_back(r);
+    }
+    va_end(cp);
+    int n = std::vfprintf(f, fmt, ap);
+    va_end(ap);
+    return n;
+}
+}  // namespace
+
+#define fprintf report_fprintf
 #define main verify_dit_reference_main
 #include "verify_dit.cpp"
 #undef main
-
-#include <cstdint>
+#undef fprintf
 
 namespace {
 
@@ -103,6 +153,31 @@ void ref_awa_block(const float* vid, int Lv, const float* txt, int TXT, int t, i
     awa_forward(v, tx, win, vW, tW, vo, to);
     for (size_t i = 0; i < vo.size(); i++) vattn[i] = vo[i];
     for (size_t i = 0; i < to.size(); i++) tattn[i] = to[i];
+}
+
+// Runs the reference's whole verify_dit main() (verify_dit.cpp:350-485: the
+// 32-layer block loop of :393-468 with its input and output layers) in the
+// directory dir, which must hold models/m5/ in the layout main reads (every
+// file must exist: main exits the process on a missing one).  Returns main's
+// exit code; the comparison lines it printed are returned as (block, cos,
+// max|diff|) triples, block -1 being the final vid_out line.  The working
+// directory is restored afterwards.
+int ref_verify_dit_main(const char* dir, int* blocks, double* cos, double* maxdiff, int cap,
+                        int* n_reports) {
+    char cwd[4096];
+    if (!getcwd(cwd, sizeof cwd)) return -100;
+    if (chdir(dir) != 0) return -101;
+    g_reports.clear();
+    int rc = verify_dit_reference_main();
+    if (chdir(cwd) != 0) return -102;
+    int n = (int)g_reports.size();
+    for (int i = 0; i < n && i < cap; i++) {
+        blocks[i] = g_reports[i].block;
+        cos[i] = g_reports[i].cos;
+        maxdiff[i] = g_reports[i].maxdiff;
+    }
+    *n_reports = n;
+    return rc;
 }
 
 }  // extern "C"

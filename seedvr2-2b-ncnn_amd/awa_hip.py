@@ -336,6 +336,25 @@ class Context:
         self._keep = gains  # alive until the stream consumed them
         return vattn, tattn
 
+    # ---- boundary casts
+    def cast_f32_to_bf16(self, src, out, stream=None):
+        """awa_cast_f32_to_bf16: fp32 device tensor -> 16-bit device tensor (bf16 bits)."""
+        if src.numel() != out.numel() or src.element_size() != 4 or out.element_size() != 2:
+            raise ValueError("cast_f32_to_bf16: 4-byte source and 2-byte output of one size")
+        rc = lib().awa_cast_f32_to_bf16(self.ptr, C.c_void_p(src.data_ptr()), C.c_void_p(out.data_ptr()),
+                                        src.numel(), _stream_ptr(stream))
+        self.check(rc, "awa_cast_f32_to_bf16")
+        return out
+
+    def cast_bf16_to_f32(self, src, out, stream=None):
+        """awa_cast_bf16_to_f32: 16-bit device tensor (bf16 bits) -> fp32 device tensor."""
+        if src.numel() != out.numel() or src.element_size() != 2 or out.element_size() != 4:
+            raise ValueError("cast_bf16_to_f32: 2-byte source and 4-byte output of one size")
+        rc = lib().awa_cast_bf16_to_f32(self.ptr, C.c_void_p(src.data_ptr()), C.c_void_p(out.data_ptr()),
+                                        src.numel(), _stream_ptr(stream))
+        self.check(rc, "awa_cast_bf16_to_f32")
+        return out
+
     # ---- the DiT block (include/dit_capi.h)
     def gemm(self, A, W, out=None, stream=None):
         """C = A W^T, bf16 [M,K] x [N,K] -> [M,N] bf16 (the block's GEMM kernel)."""
