@@ -97,6 +97,20 @@ int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf,
                  const float* h_vfreq, const float* h_tfreq, int nwin, int Lv,
                  int txt_len, awa_geom** out, awa_stream_t stream);
 
+/* The geometry of a reference struct Win (dit_vk.h:17-22), as awa::make_win
+ * returns it (awa_window.cpp:133-150) or load_win reads a win_*.bin file
+ * (dit_vk.cpp:74-93): grid t, h, w; nwin windows with slices
+ * [st,en,sh,eh,sw,ew] (h_slices, nwin x 6); vid_freq [sumf][126] in window
+ * order; txt_freq [nwin*txt_len][126].  The index is built on the host as
+ * AwaVk::forward and AwaLayer::build_window_geometry build it
+ * (awa_vk.cpp:73-88, awa_layer.cpp:110-141): windows in order, a window's
+ * tokens in (t, h, w) C order, sumf = the windows' token count, Lv = t*h*w.
+ * Rejected (AWA_EARG): slices outside the grid, a token in two windows,
+ * frequency rows whose channel pairs differ. */
+int awa_geom_from_win(awa_ctx* ctx, int t, int h, int w, int nwin, const int32_t* h_slices,
+                      const float* h_vid_freq, const float* h_txt_freq, int txt_len,
+                      awa_geom** out, awa_stream_t stream);
+
 int awa_geom_query(const awa_geom* g, awa_geom_info* info);
 
 /* Synchronous copies of the device geometry for inspection; any output may be

@@ -85,6 +85,8 @@ def lib():
                                      C.POINTER(vp), vp]
         L.awa_geom_set.argtypes = [vp, f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int,
                                    C.POINTER(vp), vp]
+        L.awa_geom_from_win.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_int, i32p, f32p, f32p, C.c_int,
+                                        C.POINTER(vp), vp]
         L.awa_geom_query.argtypes = [vp, C.POINTER(GeomInfo)]
         L.awa_geom_read.argtypes = [vp, vp, vp, vp, vp, vp, vp]
         L.awa_geom_destroy.argtypes = [vp]
@@ -301,6 +303,23 @@ class Context:
         rc = lib().awa_geom_set(self.ptr, *fp, int(nwin), int(Lv), int(txt_len), C.byref(g),
                                 _stream_ptr(stream))
         self.check(rc, "awa_geom_set")
+        return Geometry(self, g)
+
+    def geometry_from_win(self, t, h, w, slices, vid_freq, txt_freq, txt_len, stream=None):
+        """awa_geom_from_win: a reference Win (grid, nwin x 6 slices, the two
+        frequency tables), e.g. as read_win returns a win_*.bin file."""
+        sl = np.ascontiguousarray(slices, np.int32).reshape(-1, 6)
+        vf = np.ascontiguousarray(vid_freq, np.float32)
+        tf = np.ascontiguousarray(txt_freq, np.float32)
+        sizes = np.clip(sl[:, 1::2] - sl[:, 0::2], 0, None).prod(axis=1)
+        if vf.size != int(sizes.sum()) * ROPE_ROT or tf.size != sl.shape[0] * int(txt_len) * ROPE_ROT:
+            raise ValueError("geometry_from_win: frequency tables do not match the windows")
+        g = C.c_void_p()
+        rc = lib().awa_geom_from_win(self.ptr, int(t), int(h), int(w), sl.shape[0], _ptr(sl),
+                                     vf.ctypes.data_as(C.POINTER(C.c_float)),
+                                     tf.ctypes.data_as(C.POINTER(C.c_float)), int(txt_len), C.byref(g),
+                                     _stream_ptr(stream))
+        self.check(rc, "awa_geom_from_win")
         return Geometry(self, g)
 
     # ---- the op

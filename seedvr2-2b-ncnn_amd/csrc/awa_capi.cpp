@@ -283,6 +283,11 @@ hipError_t timing_mark(awa_ctx* ctx, hipStream_t s) { return event_mark(ctx, ctx
 
 namespace awa {
 
+size_t op_scratch_bytes(const GeomPlan& P, int dtype) {
+    const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * elem_size(dtype);
+    return 3 * align256(packed) + align256((size_t)P.nwin * P.txt_len * DIM * 4);
+}
+
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
                  float eps, void* d_vattn, void* d_tattn, hipStream_t s) {
@@ -291,19 +296,19 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     const size_t es = elem_size(dtype);
     const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
     const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
-    const size_t tpart_bytes = (size_t)P.nwin * P.txt_len * DIM * 4;
     // the bf16 kernel addresses vattn with 32-bit buffer offsets (and marks
     // padding rows with offsets from 2^31)
     if (dtype == AWA_BF16 && (size_t)Lv * DIM * es > 0x7fffffffu) {
         set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 2 GiB output addressing", Lv);
         return AWA_EARG;
     }
-    int rc = ensure_scratch(ctx, off_t + align256(tpart_bytes));
+    int rc = ensure_scratch(ctx, op_scratch_bytes(P, dtype));
     if (rc != AWA_OK) return rc;
     char* base = static_cast<char*>(ctx->scratch);
+    auto mark = [&]() { return timing_mark(ctx, s); };
 
     if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
-    HIPCK(ctx, timing_mark(ctx, s));
+    HIPCK(ctx, mark());
 
     PackArgs pa{};
     pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
@@ -315,7 +320,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     pa.n_tiles = P.n_tiles; pa.eps = eps;
     pa.qscale = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
     HIPCK(ctx, launch_pack(dtype, pa, s));
-    HIPCK(ctx, timing_mark(ctx, s));
+    HIPCK(ctx, mark());
 
     SdpaArgs sa{};
     sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
@@ -327,10 +332,40 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
     sa.scale_log2e = 1.0f;  // the pack kernel folded the scale into Q
     HIPCK(ctx, launch_sdpa(dtype, sa, s));
-    HIPCK(ctx, timing_mark(ctx, s));
+    HIPCK(ctx, mark());
 
     HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
-    HIPCK(ctx, timing_mark(ctx, s));
+    HIPCK(ctx, mark());
+    return AWA_OK;
+}
+
+int check_forward_args(const char* who, awa_ctx* ctx, const awa_geom* g, int dtype,
+                       const void* d_vqkv, const void* d_tqkv, int Lv, int TXT, const float* d_nq_v,
+                       const float* d_nk_v, const float* d_nq_t, const float* d_nk_t, float eps,
+                       const void* d_vattn, const void* d_tattn) {
+    if (!ctx || !g || !d_vqkv || !d_tqkv || !d_nq_v || !d_nk_v || !d_nq_t || !d_nk_t || !d_vattn ||
+        !d_tattn) {
+        set_err(ctx, "%s: null argument", who);
+        return AWA_EARG;
+    }
+    const GeomPlan& P = g->plan;
+    if (dtype != AWA_F32 && dtype != AWA_BF16) {
+        set_err(ctx, "%s: unknown dtype %d", who, dtype);
+        return AWA_EARG;
+    }
+    if (Lv != P.Lv || TXT != P.txt_len) {
+        set_err(ctx, "%s: Lv=%d TXT=%d do not match the geometry (Lv=%d TXT=%d)", who, Lv, TXT,
+                P.Lv, P.txt_len);
+        return AWA_EARG;
+    }
+    if (!(eps > 0.f)) {
+        set_err(ctx, "%s: eps must be > 0 (got %g)", who, (double)eps);
+        return AWA_EARG;
+    }
+    if (g->device != ctx->device) {
+        set_err(ctx, "%s: geometry lives on device %d, context on %d", who, g->device, ctx->device);
+        return AWA_EARG;
+    }
     return AWA_OK;
 }
 
@@ -451,6 +486,9 @@ int awa_geom_build(awa_ctx* ctx, int t, int h, int w, const int32_t num_windows[
         // them before the caller can touch the geometry.
         if ((e = hipStreamSynchronize(s)) != hipSuccess) fail(e, "sync");
     }
+    // the op's scratch for this geometry (bf16 storage), so that a first
+    // awa_forward under stream capture does not allocate
+    if (rc == AWA_OK) rc = ensure_scratch(ctx, op_scratch_bytes(P, AWA_BF16));
     if (rc != AWA_OK) {
         free_geom_buffers(g);
         delete g;
@@ -460,79 +498,78 @@ int awa_geom_build(awa_ctx* ctx, int t, int h, int w, const int32_t num_windows[
     return AWA_OK;
 }
 
-int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf, const float* h_vfreq,
-                 const float* h_tfreq, int nwin, int Lv, int txt_len, awa_geom** out,
-                 awa_stream_t stream) {
-    if (!ctx || !out || !h_cumf || !h_vfreq || !h_tfreq || !h_vidx) {
-        set_err(ctx, "awa_geom_set: null argument");
-        return AWA_EARG;
-    }
-    *out = nullptr;
-    if (nwin < 1 || nwin > MAX_WIN || Lv < 1 || txt_len < 1) {
-        set_err(ctx, "awa_geom_set: bad sizes nwin=%d Lv=%d txt=%d", nwin, Lv, txt_len);
-        return AWA_EARG;
-    }
-    // Decode the float encoding (int(x + 0.5), awa.comp:88,101) and validate.
-    std::vector<int32_t> cumf(nwin + 1);
-    for (int i = 0; i <= nwin; i++) cumf[i] = (int32_t)(h_cumf[i] + 0.5f);
+}  // extern "C"
+
+namespace {
+
+// The geometry from a decoded index: cumf [nwin+1] non-decreasing from 0,
+// vidx [cumf[nwin]] distinct tokens in [0, Lv), the frequency tables
+// [sumf][126] and [nwin*txt_len][126] with repeated channel pairs.  slices
+// (nwin x 6) and t, h, w are kept for awa_geom_read / awa_geom_query when
+// given (nullptr: zeros).  who names the entry point in error messages.
+int geom_inject(awa_ctx* ctx, const char* who, const std::vector<int32_t>& cumf,
+                const std::vector<int32_t>& vidx, const int32_t* slices, int t, int h, int w,
+                const float* h_vfreq, const float* h_tfreq, int nwin, int Lv, int txt_len,
+                awa_geom** out, hipStream_t s) {
     if (cumf[0] != 0) {
-        set_err(ctx, "awa_geom_set: cumf[0] = %d, expected 0", cumf[0]);
+        set_err(ctx, "%s: cumf[0] = %d, expected 0", who, cumf[0]);
         return AWA_EARG;
     }
     for (int i = 0; i < nwin; i++)
         if (cumf[i + 1] < cumf[i]) {
-            set_err(ctx, "awa_geom_set: cumf decreases at window %d", i);
+            set_err(ctx, "%s: cumf decreases at window %d", who, i);
             return AWA_EARG;
         }
     const int sumf = cumf[nwin];
-    if (sumf < 1 || sumf > Lv) {
-        set_err(ctx, "awa_geom_set: sumf=%d outside [1, Lv=%d]", sumf, Lv);
+    if (sumf < 1 || sumf > Lv || (int)vidx.size() != sumf) {
+        set_err(ctx, "%s: sumf=%d outside [1, Lv=%d]", who, sumf, Lv);
         return AWA_EARG;
     }
-    std::vector<int32_t> vidx(sumf);
     std::vector<uint8_t> seen(Lv, 0);
     for (int g = 0; g < sumf; g++) {
-        const float x = h_vidx[g];
-        if (!(x > -0.5f) || !(x < (float)Lv - 0.5f)) {
-            set_err(ctx, "awa_geom_set: vidx[%d] = %g outside [0, %d)", g, x, Lv);
+        const int v = vidx[g];
+        if (v < 0 || v >= Lv) {
+            set_err(ctx, "%s: vidx[%d] = %d outside [0, %d)", who, g, v, Lv);
             return AWA_EARG;
         }
-        const int v = (int)(x + 0.5f);
         if (seen[v]) {
-            set_err(ctx, "awa_geom_set: token %d appears in two windows", v);
+            set_err(ctx, "%s: token %d appears in two windows", who, v);
             return AWA_EARG;
         }
         seen[v] = 1;
-        vidx[g] = v;
     }
     for (size_t r = 0; r < (size_t)sumf; r++)
         for (int q = 0; q < NPAIR; q++)
             if (h_vfreq[r * ROPE_ROT + 2 * q] != h_vfreq[r * ROPE_ROT + 2 * q + 1]) {
-                set_err(ctx, "awa_geom_set: vfreq row %zu channel pair %d differs", r, q);
+                set_err(ctx, "%s: vfreq row %zu channel pair %d differs", who, r, q);
                 return AWA_EARG;
             }
     const size_t trows = (size_t)nwin * txt_len;
     for (size_t r = 0; r < trows; r++)
         for (int q = 0; q < NPAIR; q++)
             if (h_tfreq[r * ROPE_ROT + 2 * q] != h_tfreq[r * ROPE_ROT + 2 * q + 1]) {
-                set_err(ctx, "awa_geom_set: tfreq row %zu channel pair %d differs", r, q);
+                set_err(ctx, "%s: tfreq row %zu channel pair %d differs", who, r, q);
                 return AWA_EARG;
             }
     // Text rows shared by all windows?  (make_win repeats one table, so yes.)
     bool shared = true;
-    for (int w = 1; w < nwin && shared; w++)
-        shared = std::memcmp(h_tfreq, h_tfreq + (size_t)w * txt_len * ROPE_ROT,
+    for (int wi = 1; wi < nwin && shared; wi++)
+        shared = std::memcmp(h_tfreq, h_tfreq + (size_t)wi * txt_len * ROPE_ROT,
                              sizeof(float) * txt_len * ROPE_ROT) == 0;
 
     DeviceGuard dg(ctx->device);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     awa_geom* g = new (std::nothrow) awa_geom();
     if (!g) return AWA_EHIP;
     g->device = ctx->device;
     g->injected = true;
     GeomPlan& P = g->plan;
     P.nwin = nwin; P.Lv = Lv; P.txt_len = txt_len; P.sumf = sumf; P.cumf = cumf;
-    P.slices.assign((size_t)nwin * 6, 0);
+    if (slices) {
+        P.t = t; P.h = h; P.w = w;
+        P.slices.assign(slices, slices + (size_t)nwin * 6);
+    } else {
+        P.slices.assign((size_t)nwin * 6, 0);
+    }
     P.txt_sets = shared ? 1 : nwin;
     P.covers_all = (sumf == Lv);
     plan_tiles(P);
@@ -563,14 +600,91 @@ int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf, const f
     }
     if (rc == AWA_OK) rc = upload_plan(ctx, g, s);
     if (rc == AWA_OK) step(hipStreamSynchronize(s));
+    if (rc == AWA_OK) rc = ensure_scratch(ctx, op_scratch_bytes(P, AWA_BF16));
     if (rc != AWA_OK) {
-        if (e != hipSuccess) set_err(ctx, "awa_geom_set: %s", hipGetErrorString(e));
+        if (e != hipSuccess) set_err(ctx, "%s: %s", who, hipGetErrorString(e));
         free_geom_buffers(g);
         delete g;
         return rc;
     }
     *out = g;
     return AWA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int awa_geom_set(awa_ctx* ctx, const float* h_vidx, const float* h_cumf, const float* h_vfreq,
+                 const float* h_tfreq, int nwin, int Lv, int txt_len, awa_geom** out,
+                 awa_stream_t stream) {
+    if (!ctx || !out || !h_cumf || !h_vfreq || !h_tfreq || !h_vidx) {
+        set_err(ctx, "awa_geom_set: null argument");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    if (nwin < 1 || nwin > MAX_WIN || Lv < 1 || txt_len < 1) {
+        set_err(ctx, "awa_geom_set: bad sizes nwin=%d Lv=%d txt=%d", nwin, Lv, txt_len);
+        return AWA_EARG;
+    }
+    // Decode the float encoding (int(x + 0.5), awa.comp:88,101).
+    std::vector<int32_t> cumf(nwin + 1);
+    for (int i = 0; i <= nwin; i++) cumf[i] = (int32_t)(h_cumf[i] + 0.5f);
+    const int sumf = cumf[nwin];
+    if (sumf < 1 || sumf > Lv) {
+        set_err(ctx, "awa_geom_set: sumf=%d outside [1, Lv=%d]", sumf, Lv);
+        return AWA_EARG;
+    }
+    std::vector<int32_t> vidx(sumf);
+    for (int g = 0; g < sumf; g++) {
+        const float x = h_vidx[g];
+        if (!(x > -0.5f) || !(x < (float)Lv - 0.5f)) {
+            set_err(ctx, "awa_geom_set: vidx[%d] = %g outside [0, %d)", g, x, Lv);
+            return AWA_EARG;
+        }
+        vidx[g] = (int)(x + 0.5f);
+    }
+    return geom_inject(ctx, "awa_geom_set", cumf, vidx, nullptr, 0, 0, 0, h_vfreq, h_tfreq, nwin, Lv,
+                       txt_len, out, reinterpret_cast<hipStream_t>(stream));
+}
+
+int awa_geom_from_win(awa_ctx* ctx, int t, int h, int w, int nwin, const int32_t* h_slices,
+                      const float* h_vid_freq, const float* h_txt_freq, int txt_len, awa_geom** out,
+                      awa_stream_t stream) {
+    if (!ctx || !out || !h_slices || !h_vid_freq || !h_txt_freq) {
+        set_err(ctx, "awa_geom_from_win: null argument");
+        return AWA_EARG;
+    }
+    *out = nullptr;
+    if (t < 1 || h < 1 || w < 1 || (long)t * h * w > (1L << 24) || nwin < 1 || nwin > MAX_WIN ||
+        txt_len < 1) {
+        set_err(ctx, "awa_geom_from_win: bad sizes t=%d h=%d w=%d nwin=%d txt=%d", t, h, w, nwin, txt_len);
+        return AWA_EARG;
+    }
+    // The index of awa_vk.cpp:73-88 / awa_layer.cpp:116-128: windows in
+    // order, tokens of a window in (t, h, w) C order.
+    const int ext[3] = {t, h, w};
+    std::vector<int32_t> cumf(nwin + 1, 0), vidx;
+    for (int wi = 0; wi < nwin; wi++) {
+        const int32_t* sl = h_slices + (size_t)wi * 6;
+        for (int a = 0; a < 3; a++)
+            if (sl[2 * a] < 0 || sl[2 * a] > sl[2 * a + 1] || sl[2 * a + 1] > ext[a]) {
+                set_err(ctx, "awa_geom_from_win: window %d axis %d slice [%d, %d) outside [0, %d]", wi, a,
+                        sl[2 * a], sl[2 * a + 1], ext[a]);
+                return AWA_EARG;
+            }
+        const long f = (long)(sl[1] - sl[0]) * (sl[3] - sl[2]) * (sl[5] - sl[4]);
+        if (cumf[wi] + f > (long)t * h * w) {
+            set_err(ctx, "awa_geom_from_win: windows hold more tokens than the grid");
+            return AWA_EARG;
+        }
+        cumf[wi + 1] = cumf[wi] + (int32_t)f;
+        for (int lt = sl[0]; lt < sl[1]; lt++)
+            for (int lh = sl[2]; lh < sl[3]; lh++)
+                for (int lw = sl[4]; lw < sl[5]; lw++) vidx.push_back((lt * h + lh) * w + lw);
+    }
+    return geom_inject(ctx, "awa_geom_from_win", cumf, vidx, h_slices, t, h, w, h_vid_freq, h_txt_freq,
+                       nwin, t * h * w, txt_len, out, reinterpret_cast<hipStream_t>(stream));
 }
 
 int awa_geom_query(const awa_geom* g, awa_geom_info* info) {
@@ -612,29 +726,9 @@ void awa_geom_destroy(awa_geom* g) {
 int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                 int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
                 const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, awa_stream_t stream) {
-    if (!ctx || !g || !d_vqkv || !d_tqkv || !d_nq_v || !d_nk_v || !d_nq_t || !d_nk_t || !d_vattn ||
-        !d_tattn) {
-        set_err(ctx, "awa_forward: null argument");
-        return AWA_EARG;
-    }
-    const GeomPlan& P = g->plan;
-    if (dtype != AWA_F32 && dtype != AWA_BF16) {
-        set_err(ctx, "awa_forward: unknown dtype %d", dtype);
-        return AWA_EARG;
-    }
-    if (Lv != P.Lv || TXT != P.txt_len) {
-        set_err(ctx, "awa_forward: Lv=%d TXT=%d do not match the geometry (Lv=%d TXT=%d)", Lv, TXT,
-                P.Lv, P.txt_len);
-        return AWA_EARG;
-    }
-    if (!(eps > 0.f)) {
-        set_err(ctx, "awa_forward: eps must be > 0 (got %g)", (double)eps);
-        return AWA_EARG;
-    }
-    if (g->device != ctx->device) {
-        set_err(ctx, "awa_forward: geometry lives on device %d, context on %d", g->device, ctx->device);
-        return AWA_EARG;
-    }
+    const int rc = check_forward_args("awa_forward", ctx, g, dtype, d_vqkv, d_tqkv, Lv, TXT, d_nq_v,
+                                      d_nk_v, d_nq_t, d_nk_t, eps, d_vattn, d_tattn);
+    if (rc != AWA_OK) return rc;
     DeviceGuard dg(ctx->device);
     return forward_impl(ctx, g, dtype, d_vqkv, d_tqkv, d_nq_v, d_nk_v, d_nq_t, d_nk_t, eps, d_vattn,
                         d_tattn, reinterpret_cast<hipStream_t>(stream));

@@ -165,6 +165,15 @@ struct DeviceGuard {
 // Grows a device buffer (freeing the old one, which waits for its users).
 hipError_t ensure_buffer(void** buf, size_t* have, size_t need);
 hipError_t event_mark(awa_ctx* ctx, std::vector<hipEvent_t>& list, hipStream_t s);
+// Argument checks of awa_forward (and its allocation-free variant); who
+// names the entry point in the error message.
+int check_forward_args(const char* who, awa_ctx* ctx, const awa_geom* g, int dtype,
+                       const void* d_vqkv, const void* d_tqkv, int Lv, int TXT, const float* d_nq_v,
+                       const float* d_nk_v, const float* d_nq_t, const float* d_nk_t, float eps,
+                       const void* d_vattn, const void* d_tattn);
+// Bytes of scratch the op needs for a geometry and storage type: packed Q, K
+// and V tiles, then the per-window text partials, each 256-byte aligned.
+size_t op_scratch_bytes(const GeomPlan& P, int dtype);
 // awa_forward without argument checks (shared with the block).
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,

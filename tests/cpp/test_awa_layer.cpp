@@ -3,15 +3,22 @@
 // (src/test_awa_layer.cpp): prints the checks and returns non-zero on failure.
 //
 //  1. AwaLayer with device-built geometry vs AwaLayer with the same geometry
-//     injected through set_window_geometry: identical outputs (fp32 and bf16).
-//  2. AwaVk (host vectors) vs AwaLayer fp32: identical outputs.
+//     injected through set_window_geometry, and vs AwaLayer reading it from a
+//     win_*.bin file (build_window_geometry, awa_layer.cpp:110-141):
+//     identical outputs (fp32 and bf16).
+//  2. AwaVk (host vectors) vs AwaLayer fp32: identical outputs, with the
+//     geometry handle and with a reference Win record (awa_vk.h:40-45).
 //  3. Error paths return -1 / false.
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
+#include <unistd.h>
 
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "awa_layer.hpp"
@@ -36,7 +43,28 @@ static uint16_t to_bf16(float f) {
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
+// A window file in load_win's layout (dit_vk.cpp:74-93) from a geometry.
+static bool write_win(const std::string& path, int t, int h, int w, const int32_t nw[3],
+                      const std::vector<int32_t>& slices, const std::vector<float>& vf,
+                      const std::vector<float>& tf) {
+    std::ofstream f(path, std::ios::binary);
+    const int64_t nwin = (int64_t)slices.size() / 6;
+    const int64_t hdr[10] = {t, h, w, nw[0], nw[1], nw[2], 0, 0, 0, nwin};
+    f.write(reinterpret_cast<const char*>(hdr), sizeof hdr);
+    for (int32_t v : slices) {
+        const int64_t x = v;
+        f.write(reinterpret_cast<const char*>(&x), 8);
+    }
+    f.write(reinterpret_cast<const char*>(vf.data()), vf.size() * 4);
+    f.write(reinterpret_cast<const char*>(tf.data()), tf.size() * 4);
+    return (bool)f;
+}
+
 int main() {
+    char tmpl[] = "/tmp/awa_win_XXXXXX";
+    const char* tmpdir = mkdtemp(tmpl);
+    if (!tmpdir) return 2;
+    const std::string win_dir = std::string(tmpdir) + "/";
     const int t = 1, h = 12, w = 20, TXT = 9, Lv = t * h * w;
     const int32_t nw[3] = {4, 3, 3};
     std::mt19937 rng(123);
@@ -84,6 +112,22 @@ int main() {
         std::vector<float> fcumf(cumf.begin(), cumf.end()), fvidx(vidx.begin(), vidx.end());
         check(injected.set_window_geometry(fvidx, fcumf, vf, tf, info.nwin, Lv, TXT) == 0,
               "set_window_geometry with the device geometry's arrays");
+        std::vector<int32_t> slices((size_t)info.nwin * 6);
+        awa_geom_read(built.context(), built.geometry(), slices.data(), nullptr, nullptr, nullptr, nullptr);
+        const std::string wpath = win_dir + (win_type == 0 ? "win_nonshifted.bin" : "win_shifted.bin");
+        check(write_win(wpath, t, h, w, nw, slices, vf, tf), "write the window file");
+        seedvr2::AwaLayer fromfile;
+        fromfile.set_config(win_type, Lv, TXT);
+        fromfile.set_win_dir(win_dir);
+        fromfile.set_qk_norm_device(d_g, d_g + 128, d_g + 256, d_g + 384);
+        check(fromfile.build_window_geometry() == 0, "build_window_geometry from the window file");
+        seedvr2::Win win;
+        check(seedvr2::load_win(wpath, TXT, win) && win.nwin == info.nwin && win.t == t && win.h == h &&
+                  win.w == w, "load_win");
+        seedvr2::AwaLayer nofile;
+        nofile.set_config(win_type, Lv, TXT);
+        nofile.set_win_dir(win_dir + "missing/");
+        check(nofile.build_window_geometry() == -1, "build_window_geometry without the file returns -1");
         std::vector<float> bad = fvidx;
         bad[1] = bad[0];
         seedvr2::AwaLayer rejecting;
@@ -106,6 +150,13 @@ int main() {
             char msg[128];
             std::snprintf(msg, sizeof msg, "win_type %d %s: built == injected geometry", win_type, bf ? "bf16" : "fp32");
             check(r1 == 0 && r2 == 0 && a == b && ta == tb, msg);
+            int r3 = fromfile.forward(v, vqkv.size() * es, tq, tqkv.size() * es, d_o2, d_to2, bf);
+            CK(hipDeviceSynchronize());
+            CK(hipMemcpy(b.data(), d_o2, b.size(), hipMemcpyDeviceToHost));
+            CK(hipMemcpy(tb.data(), d_to2, tb.size(), hipMemcpyDeviceToHost));
+            std::snprintf(msg, sizeof msg, "win_type %d %s: built == window-file geometry", win_type,
+                          bf ? "bf16" : "fp32");
+            check(r3 == 0 && a == b && ta == tb, msg);
             if (!bf) {
                 seedvr2::AwaVk vk;
                 check(vk.init(0), "AwaVk::init");
@@ -116,6 +167,12 @@ int main() {
                 std::snprintf(msg, sizeof msg, "win_type %d: AwaVk host vectors == AwaLayer fp32", win_type);
                 check(ok && std::memcmp(vo.data(), a.data(), a.size()) == 0 &&
                           std::memcmp(to.data(), ta.data(), ta.size()) == 0, msg);
+                std::vector<float> wo, wto;
+                ok = vk.forward(vqkv, tqkv, win, g0, g1, g2, g3, Lv, TXT, wo, wto) &&
+                     vk.forward(vqkv, tqkv, win, g0, g1, g2, g3, Lv, TXT, vo, to);  // cached geometry
+                std::snprintf(msg, sizeof msg, "win_type %d: AwaVk with a Win record == AwaLayer fp32", win_type);
+                check(ok && std::memcmp(wo.data(), a.data(), a.size()) == 0 &&
+                          std::memcmp(wto.data(), ta.data(), ta.size()) == 0 && wo == vo && wto == to, msg);
                 std::vector<float> short_v(vqkv.begin(), vqkv.end() - 1);
                 check(!vk.forward(short_v, tqkv, built.geometry(), g0, g1, g2, g3, Lv, TXT, vo, to),
                       "AwaVk::forward rejects a short vqkv");
@@ -124,6 +181,8 @@ int main() {
     }
     (void)hipFree(d_v); (void)hipFree(d_t); (void)hipFree(d_v16); (void)hipFree(d_t16); (void)hipFree(d_g);
     (void)hipFree(d_o1); (void)hipFree(d_o2); (void)hipFree(d_to1); (void)hipFree(d_to2);
+    for (const char* n : {"win_nonshifted.bin", "win_shifted.bin"}) unlink((win_dir + n).c_str());
+    rmdir(tmpdir);
     std::printf(fails ? "FAIL (%d)\n" : "ALL PASS\n", fails);
     return fails ? 1 : 0;
 }

@@ -299,3 +299,54 @@ def test_cpp_host_mirror():
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("name,shifted", [("cfg2_1080p", 1), ("cfg4_ragged", 0), ("cfg5_frames", 1),
+                                          ("cfg0_360p", 0)])
+def test_geometry_from_reference_win_file(oracle, ctx, awa, tmp_path, name, shifted):
+    """A win_*.bin file in load_win's layout (dit_vk.cpp:74-93), read by
+    dit_read_win and bound through awa_geom_from_win (the reference's Win,
+    awa_vk.h:40-45), gives the same geometry as awa_geom_build and the same
+    output bits."""
+    import torch
+    from model_files import write_win
+    grid, nw, txt, seed, frac = CONFIGS[name]
+    og = oracle.Geometry(*grid, nw, txt, shifted)
+    path = tmp_path / "win.bin"
+    write_win(str(path), [*grid, *nw, 0, 0, 0, og.nwin], og.slices, og.vid_freq, og.txt_freq)
+    d = awa.read_win(path, txt)
+    gw = ctx.geometry_from_win(*grid, d["slices"], d["vid_freq"], d["txt_freq"], txt)
+    gb = ctx.build_geometry(*grid, nw, txt, shifted)
+    rw, rb = gw.read(), gb.read()
+    for k in ("slices", "cumf", "vidx"):
+        assert np.array_equal(rw[k], rb[k]), k
+    for k in ("vid_freq", "txt_freq"):
+        assert np.array_equal(rw[k].view(np.uint32), rb[k].view(np.uint32)), k
+    assert gw.info() == gb.info()
+    vqkv, tqkv, gains = seeded_awa_inputs(og.Lv, txt, seed, frac)
+    dtypes = [torch.bfloat16] + ([torch.float32] if og.Lv <= 3200 else [])
+    for dt in dtypes:
+        note(f"win file {name} shifted={shifted} {dt}")
+        a = run_gpu(ctx, gw, vqkv, tqkv, gains, dt)
+        b = run_gpu(ctx, gb, vqkv, tqkv, gains, dt)
+        assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
+        assert np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+    gw.close()
+    gb.close()
+
+
+def test_geometry_from_win_rejects(oracle, ctx, awa):
+    """Slices outside the grid and a token in two windows are refused."""
+    og = oracle.Geometry(1, 23, 27, (4, 3, 3), 58, 0)
+    def vf_for(sl):
+        return np.zeros((int(np.prod(sl[:, 1::2] - sl[:, 0::2], axis=1).sum()), 126), np.float32)
+
+    sl = og.slices.copy()
+    sl[0, 3] = 24  # h end beyond the grid
+    with pytest.raises(awa.AwaError, match="outside"):
+        ctx.geometry_from_win(1, 23, 27, sl, vf_for(sl), og.txt_freq, 58)
+    sl = og.slices.copy()
+    s0 = sl[0]
+    sl[1] = [s0[0], s0[0] + 1, s0[2], s0[2] + 1, s0[4], s0[4] + 1]  # window 0's first token again
+    with pytest.raises(awa.AwaError, match="two windows"):
+        ctx.geometry_from_win(1, 23, 27, sl, vf_for(sl), og.txt_freq, 58)
