@@ -135,6 +135,23 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
                 const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
                 float eps, void* d_vattn, void* d_tattn, awa_stream_t stream);
 
+/* awa_forward without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as awa_forward; the scratch is a fixed
+ * device array of AWA_NOALLOC_SCRATCH_MIB MiB that the library holds on every
+ * device it runs on until the process ends (awa_create looks up its address).
+ * Geometries whose scratch exceeds it are rejected with AWA_EARG (1080p bf16
+ * needs 107 MiB, the 71 x 97 grid with 77 text rows 143 MiB; fp32 storage
+ * needs about twice as much).  No per-phase timing events are recorded.  All
+ * calls on one device share the array: calls that overlap in time on one
+ * device race. */
+enum { AWA_NOALLOC_SCRATCH_MIB = 160 };
+int awa_forward_noalloc(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
+                        const void* d_tqkv, int Lv, int TXT, const float* d_nq_v,
+                        const float* d_nk_v, const float* d_nq_t, const float* d_nk_t, float eps,
+                        void* d_vattn, void* d_tattn, awa_stream_t stream);
+
 /* AwaVk::forward (awa_vk.cpp:62-199): fp32 host vectors in and out, computed
  * on the device, synchronous.  Returns 0 / error code instead of bool. */
 int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv,

@@ -93,6 +93,8 @@ def lib():
         L.awa_geom_destroy.restype = None
         L.awa_forward.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
                                   C.c_float, vp, vp, vp]
+        L.awa_forward_noalloc.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
+                                          C.c_float, vp, vp, vp]
         L.awa_forward_host.argtypes = [vp, vp, f32p, f32p, C.c_int, C.c_int, f32p, f32p, f32p, f32p,
                                        C.c_float, f32p, f32p]
         L.awa_timing_enable.argtypes = [vp, C.c_int]
@@ -324,8 +326,10 @@ class Context:
 
     # ---- the op
     def forward(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, eps=1e-5, vattn=None, tattn=None,
-                stream=None):
-        """AwaLayer::forward: torch tensors on the device; returns (vattn, tattn)."""
+                stream=None, noalloc=False):
+        """AwaLayer::forward: torch tensors on the device; returns (vattn, tattn).
+        noalloc=True calls awa_forward_noalloc (the library's fixed device
+        scratch instead of the context's)."""
         import torch
         if vqkv.dtype == torch.bfloat16:
             dtype = AWA_BF16
@@ -346,12 +350,13 @@ class Context:
             vattn = torch.empty((Lv, DIM), dtype=vqkv.dtype, device=vqkv.device)
         if tattn is None:
             tattn = torch.empty((TXT, DIM), dtype=vqkv.dtype, device=vqkv.device)
-        rc = lib().awa_forward(self.ptr, geom.ptr, dtype, C.c_void_p(vqkv.data_ptr()),
+        fn = lib().awa_forward_noalloc if noalloc else lib().awa_forward
+        rc = fn(self.ptr, geom.ptr, dtype, C.c_void_p(vqkv.data_ptr()),
                                C.c_void_p(tqkv.data_ptr()), Lv, TXT,
                                *[C.c_void_p(g.data_ptr()) for g in gains], float(eps),
                                C.c_void_p(vattn.data_ptr()), C.c_void_p(tattn.data_ptr()),
                                _stream_ptr(stream))
-        self.check(rc, "awa_forward")
+        self.check(rc, "awa_forward_noalloc" if noalloc else "awa_forward")
         self._keep = gains  # alive until the stream consumed them
         return vattn, tattn
 

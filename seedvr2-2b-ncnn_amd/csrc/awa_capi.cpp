@@ -290,7 +290,7 @@ size_t op_scratch_bytes(const GeomPlan& P, int dtype) {
 
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
-                 float eps, void* d_vattn, void* d_tattn, hipStream_t s) {
+                 float eps, void* d_vattn, void* d_tattn, hipStream_t s, void* ext_scratch) {
     const GeomPlan& P = g->plan;
     const int Lv = P.Lv;
     const size_t es = elem_size(dtype);
@@ -302,10 +302,15 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
         set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 2 GiB output addressing", Lv);
         return AWA_EARG;
     }
-    int rc = ensure_scratch(ctx, op_scratch_bytes(P, dtype));
-    if (rc != AWA_OK) return rc;
-    char* base = static_cast<char*>(ctx->scratch);
-    auto mark = [&]() { return timing_mark(ctx, s); };
+    char* base = static_cast<char*>(ext_scratch);
+    if (!base) {
+        int rc = ensure_scratch(ctx, op_scratch_bytes(P, dtype));
+        if (rc != AWA_OK) return rc;
+        base = static_cast<char*>(ctx->scratch);
+    }
+    // per-phase events only for the context's own scratch: creating events
+    // may allocate, which the caller-provided scratch path must not
+    auto mark = [&]() { return ext_scratch ? hipSuccess : timing_mark(ctx, s); };
 
     if (!P.covers_all) HIPCK(ctx, launch_zero(d_vattn, (size_t)Lv * DIM * es, s));
     HIPCK(ctx, mark());
@@ -381,6 +386,12 @@ int awa_create(awa_ctx** out, int hip_device) {
     awa_ctx* ctx = new (std::nothrow) awa_ctx();
     if (!ctx) return AWA_EHIP;
     ctx->device = hip_device;
+    {
+        // the allocation-free entry's device array: its address on this
+        // device, looked up once per device with the device current
+        DeviceGuard dg(hip_device);
+        ctx->noalloc_status = noalloc_resolve(hip_device);
+    }
     *out = ctx;
     return AWA_OK;
 }

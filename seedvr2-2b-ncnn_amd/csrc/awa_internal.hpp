@@ -118,6 +118,7 @@ struct GeomPlan {
 struct awa_ctx {
     int device = 0;
     std::string err;
+    hipError_t noalloc_status = hipSuccess;  // lookup of the allocation-free entry's scratch
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     // Per-phase timing (awa_timing_enable): 4 events per recorded call,
@@ -174,10 +175,18 @@ int check_forward_args(const char* who, awa_ctx* ctx, const awa_geom* g, int dty
 // Bytes of scratch the op needs for a geometry and storage type: packed Q, K
 // and V tiles, then the per-window text partials, each 256-byte aligned.
 size_t op_scratch_bytes(const GeomPlan& P, int dtype);
-// awa_forward without argument checks (shared with the block).
+// awa_forward without argument checks (shared with the block).  ext_scratch:
+// nullptr uses the context's scratch (grown on demand, per-phase events when
+// timing is on); otherwise a caller-provided device buffer of at least
+// op_scratch_bytes, and nothing is allocated or recorded.
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
-                 float eps, void* d_vattn, void* d_tattn, hipStream_t s);
+                 float eps, void* d_vattn, void* d_tattn, hipStream_t s, void* ext_scratch = nullptr);
+// The allocation-free entry's per-device scratch (awa_noalloc.hip):
+// noalloc_resolve looks up the device address of the current device's copy
+// (call with that device current); noalloc_scratch returns it, or nullptr.
+hipError_t noalloc_resolve(int device);
+void* noalloc_scratch(int device);
 
 // Kernel launchers (defined in the .hip files).
 hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s);
