@@ -150,8 +150,8 @@ def write_graph(root, out_param, out_bin, n_layers, mm_layers, ada_compose=True,
         for f in "vt":
             ip(f"{br(i, f)}_out", f"{f}_attn_{i}", f"{f}_outp_{i}", f"out_{i}_{f}")
         for f in "vt":
-            a_g, m_sc, m_sh, m_g = ada[i, f][2:]
-            lines.append(f"BinaryOp g_{i}_{f} 2 1 {f}_outp_{i} {a_g} {f}_g_{i} 0=2")
+            lines.append(f"BinaryOp g_{i}_{f} 2 1 {f}_outp_{i} {ada[i, f][2]} {f}_g_{i} 0=2")
+        for f in "vt":
             lines.append(f"BinaryOp res_{i}_{f} 2 1 {f}_g_{i} {f}_cur_{i} {f}_cur_{i}_a 0=0")
         for f in "vt":
             a_g, m_sc, m_sh, m_g = ada[i, f][2:]

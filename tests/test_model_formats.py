@@ -216,3 +216,51 @@ def test_merged_graph_errors(hip, tmp_path):
         hip.graph_file_info(gp, long_)
     with pytest.raises(hip.HostError, match="not an ncnn"):
         hip.graph_file_info(gb, gb)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("layout", ["adacompose", "inputs"])
+def test_graph_layout_matches_reference_exporter(hip, layout):
+    """The reference's own exporter (export/export_dit_graph.py, run by
+    tests/golden/make_graph_golden.py) wrote graph_ref_2layer.json from a
+    seeded two-layer model directory.  write_graph on the same directory
+    reproduces its .param line for line and token for token (the exporter
+    pads with runs of spaces, which ncnn's tokenizer ignores) and its .bin
+    blob for blob (offset, tag, size, SHA-256); the product's graph readers
+    load the reference-written .param and return the directory's weights."""
+    import importlib.util
+    import json
+    import tempfile
+    spec = importlib.util.spec_from_file_location("mkg", os.path.join(GOLDEN, "make_graph_golden.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    gold = json.load(open(os.path.join(GOLDEN, "graph_ref_2layer.json")))
+    ref = gold["layouts"][layout]
+    ada = layout == "adacompose"
+    n_layers, mm = gold["n_layers"], 10   # the exporter's MM_LAYERS
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    with tempfile.TemporaryDirectory(dir=shm) as tmp:
+        model = os.path.join(tmp, "m5")
+        mk.make_model_dir(model)
+        gp, gb = os.path.join(tmp, "g.param"), os.path.join(tmp, "g.bin")
+        write_graph(model, gp, gb, n_layers, mm, ada_compose=ada)
+        text = open(gp).read()
+        assert [ln.split() for ln in text.splitlines()] == [ln.split() for ln in ref["param"]]
+        man = mk.manifest(text, open(gb, "rb").read())
+        for got, want in zip(man["parts"], ref["bin"]["parts"]):
+            assert got == want, (got, want)
+        assert man == ref["bin"]
+
+        ref_param = os.path.join(tmp, "ref.param")
+        with open(ref_param, "w") as f:
+            f.write("\n".join(ref["param"]) + "\n")
+        mm_arg = -1 if ada else mm   # AdaCompose's 2= carries the exporter's MM_LAYERS (10)
+        assert hip.graph_file_info(ref_param, gb, mm_arg)[:2] == (n_layers, mm)
+        for name, bias in (("b0_vid_qkv", False), ("b1_txt_out", True), ("b1_vid_mlp_out", False),
+                           ("vid_out_proj", True), ("txt_in", True)):
+            w, b = hip.read_graph_weight(ref_param, gb, name, mm_arg)
+            W, B = hip.read_linear(os.path.join(model, name), bias)
+            assert np.array_equal(w, W) and (B is None or np.array_equal(b, B)), name
+        for name in ("b1_txt_nk", "vid_out_norm_w") + (("b0_vid_mlp_gate",) if ada else ()):
+            w, _ = hip.read_graph_weight(ref_param, gb, name, mm_arg)
+            assert np.array_equal(w, hip.read_raw_f(os.path.join(model, name + ".bin")).ravel()), name
