@@ -42,6 +42,16 @@ def measured_traffic():
         return {}
 
 
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+# The other workloads of the op, timed beside the headline one:
+#   name: grid, num_windows, txt, shifted, storage, seed, outlier fraction
+CONFIGS = {
+    "cfg0_360p_fp32": ((1, 23, 27), (4, 3, 3), 58, 0, "f32", 0, 0.0),
+    "cfg1_720p_bf16": ((1, 45, 53), (4, 3, 3), 58, 1, "bf16", 1, 0.0),
+    "cfg4_ragged_bf16": ((1, 71, 97), (1, 4, 4), 77, 1, "bf16", 4, 0.01),
+}
+
+
 def sdpa_flops(S_list):
     # QK^T + PV over each window's S = f + TXT rows, 20 heads x 128
     return sum(4.0 * 128 * 20 * s * s for s in S_list)
@@ -80,6 +90,79 @@ def cpu_baseline(vq_bf16_f32, tq_bf16_f32, gains):
             "dit_step_extrapolated": cpu_step_extrapolated(O, vq_bf16_f32, tq_bf16_f32, gains, nt)}
 
 
+def config_runs(ctx, torch, steps, cpu=True):
+    """Each extra workload: ms per AWA layer (eager launches, wall clock), the
+    attention kernel's MFMA fraction (fp32 peak for fp32 storage), the pack
+    and text-average passes against HBM, and the oracle's CPU attention on
+    the same layer (1 thread and all host cores, up to 16)."""
+    import numpy as np
+    res = {}
+    dev = torch.device("cuda:0")
+    for name, (grid, nw, txt, sh, store, seed, frac) in CONFIGS.items():
+        rng = np.random.default_rng(seed)
+        Lv = grid[0] * grid[1] * grid[2]
+        vqn = rng.standard_normal((Lv, 7680), dtype=np.float32)
+        tqn = rng.standard_normal((txt, 7680), dtype=np.float32)
+        if frac > 0:
+            for a in (vqn, tqn):
+                a[rng.random(a.shape) < frac] *= 8.0
+        gains_np = [(1.0 + 0.02 * rng.standard_normal(128)).astype(np.float32) for _ in range(4)]
+        dt = torch.float32 if store == "f32" else torch.bfloat16
+        vq = torch.from_numpy(vqn).to(dev, dt)
+        tq = torch.from_numpy(tqn).to(dev, dt)
+        gains = [torch.from_numpy(g).to(dev) for g in gains_np]
+        va = torch.empty((Lv, 2560), dtype=dt, device=dev)
+        ta = torch.empty((txt, 2560), dtype=dt, device=dev)
+        g = ctx.build_geometry(*grid, nw, txt, sh)
+        d = g.read()
+        S = [int(c1 - c0) + txt for c0, c1 in zip(d["cumf"][:-1], d["cumf"][1:])]
+        fl = sdpa_flops(S)
+        for _ in range(3):
+            ctx.forward(g, vq, tq, *gains, eps=1e-5, vattn=va, tattn=ta)
+        torch.cuda.synchronize()
+        ctx.timing(True)
+        ctx.timing_read()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ctx.forward(g, vq, tq, *gains, eps=1e-5, vattn=va, tattn=ta)
+        torch.cuda.synchronize()
+        layer_ms = (time.perf_counter() - t0) * 1e3 / steps
+        mp, ma, mt, c = ctx.timing_read()
+        ctx.timing(False)
+        es = 4 if store == "f32" else 2
+        peak = PEAK_FP32_TFLOPS if store == "f32" else PEAK_BF16_TFLOPS
+        attn_s = ma * 1e-3 / c
+        tfl = fl / attn_s / 1e12
+        qk_bytes = 2 * (Lv + txt) * 2 * 2560 * es
+        co_bytes = (g.info()["nwin"] + 1) * txt * 2560 * 4
+        r = {"grid": list(grid), "num_windows": list(nw), "txt_len": txt, "shifted": bool(sh),
+             "storage": store, "nwin": g.info()["nwin"], "ms_per_layer": round(layer_ms, 4),
+             "phases_us": {"pack": round(mp * 1e3 / c, 2), "attention": round(attn_s * 1e6, 2),
+                           "text_average": round(mt * 1e3 / c, 2)},
+             "attention_roofline": {"bound": "mfma", "achieved": round(tfl, 1), "peak": peak,
+                                    "unit": "TFLOP/s", "frac": round(tfl / peak, 4),
+                                    "gflop_per_launch": round(fl / 1e9, 3)},
+             "hbm_qknorm_rope_frac": round(qk_bytes / (mp * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4),
+             "hbm_text_average_frac": round(co_bytes / (mt * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4)}
+        if cpu:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle as O
+            og = O.Geometry(*grid, nw, txt, sh)
+            vqf, tqf = vq.float().cpu().numpy(), tq.float().cpu().numpy()
+            nt = max(1, min(16, os.cpu_count() or 1))
+            t0 = time.perf_counter()
+            O.awa_forward(vqf, tqf, og, *gains_np, eps=1e-5, nthreads=1)
+            t1 = time.perf_counter()
+            O.awa_forward(vqf, tqf, og, *gains_np, eps=1e-5, nthreads=nt)
+            t2 = time.perf_counter()
+            r["cpu_baseline"] = {"value": round((t1 - t0) * 1e3, 1), "unit": "ms per AWA layer",
+                                 "cores": 1, "kind": "port",
+                                 "omp_all_cores": {"value": round((t2 - t1) * 1e3, 1), "threads": nt}}
+        g.close()
+        res[name] = r
+    return res
+
+
 def cpu_step_extrapolated(O, vq, tq, gains, nt, rows=256, mlp=6912):
     """CPU 32-layer step, extrapolated: the oracle's fp32 GEMMs of one layer
     (qkv 2560->7680, out 2560->2560, MLP in and gate 2560->6912, MLP out
@@ -113,7 +196,7 @@ def cpu_step_extrapolated(O, vq, tq, gains, nt, rows=256, mlp=6912):
             "reference_published_cpu_dit_s": 358.96}
 
 
-def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912):
+def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912, graph=True):
     """32-layer DiT step at 1080p: time embedding (t=1000) + 32 layers, layers
     0-9 with separate video/text branches, 10-31 shared, even layers unshifted,
     odd shifted; weights N(0, 0.02) bf16 resident in HBM (42 branches)."""
@@ -168,6 +251,22 @@ def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912):
     assert bool(torch.isfinite(x).all()), "non-finite hidden state"
     step_s = (t1 - t0) / steps
 
+    M = Lv + TXT
+    gemm_flops = 32 * 2 * M * 2560 * (7680 + 2560 + 3 * mlp)
+    res = {"value": round(step_s, 5), "unit": "s per 32-layer DiT step", "steps": steps,
+           "awa_ms_per_layer_in_step": round(ms_awa / steps / 32, 4),
+           "warmup": warmup, "mlp": mlp,
+           "txt_semantics": "text rows processed on every layer (merged-graph order)",
+           "per_step_ms": {"gemm": round(ms_gemm / steps, 3), "awa": round(ms_awa / steps, 3),
+                           "norm_ada_eltwise": round(ms_elt / steps, 3)},
+           "gemm_tflops": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12, 1),
+           "gemm_frac_of_bf16_peak": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+           "layers_timed": nl}
+    if not graph:
+        for g in geoms:
+            g.close()
+        return res
+
     # the same step captured as one HIP graph (the launches above, recorded on a
     # side stream) and replayed; each step starts from x0, so a replay must equal
     # the eager result bit for bit
@@ -178,32 +277,24 @@ def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912):
         one_step()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
+    g_step = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_step, stream=side):
         one_step()
     x.zero_()
     torch.cuda.synchronize()
-    graph.replay()
+    g_step.replay()
     torch.cuda.synchronize()
     assert torch.equal(x, x_eager), "graph replay differs from the eager step"
     t0 = time.perf_counter()
     for _ in range(steps):
-        graph.replay()
+        g_step.replay()
     torch.cuda.synchronize()
     graph_s = (time.perf_counter() - t0) / steps
-    del graph
-    M = Lv + TXT
-    gemm_flops = 32 * 2 * M * 2560 * (7680 + 2560 + 3 * mlp)
+    del g_step
     for g in geoms:
         g.close()
-    return {"value": round(step_s, 5), "unit": "s per 32-layer DiT step", "steps": steps,
-            "warmup": warmup, "mlp": mlp, "graph_replay_s": round(graph_s, 5),
-            "txt_semantics": "text rows processed on every layer (merged-graph order)",
-            "per_step_ms": {"gemm": round(ms_gemm / steps, 3), "awa": round(ms_awa / steps, 3),
-                            "norm_ada_eltwise": round(ms_elt / steps, 3)},
-            "gemm_tflops": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12, 1),
-            "gemm_frac_of_bf16_peak": round(gemm_flops / (ms_gemm / steps * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "layers_timed": nl}
+    res["graph_replay_s"] = round(graph_s, 5)
+    return res
 
 
 def main():
@@ -214,6 +305,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the 32-layer DiT step")
     ap.add_argument("--dit-steps", type=int, default=5)
+    ap.add_argument("--no-configs", action="store_true", help="skip the 360p fp32, 720p and ragged workloads")
+    ap.add_argument("--no-mlp10240", action="store_true", help="skip the MLP-10240 DiT step variant")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (4 times) to calibrate the "
                          "FETCH_SIZE/WRITE_SIZE counters, then exit")
@@ -399,8 +492,27 @@ def main():
                             "measured_GBs": round(pack_bytes / pack_avg_s / 1e9, 1) if pack_bytes else None},
         "per_variant": per_variant,
     }
+    # the text average against HBM: (nwin + 1) TXT 2560 fp32 bytes per launch
+    co_bytes = [(infos[k]["nwin"] + 1) * TXT * 2560 * 4 for k in range(2)]
+    text_avg_s = ms_text * 1e-3 / calls
+    out["hbm_text_average"] = {"algorithmic_bytes": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls),
+                               "achieved_GBs": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls
+                                                     / text_avg_s / 1e9, 1),
+                               "frac": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls
+                                             / text_avg_s / 1e9 / PEAK_HBM_GBS, 4)}
+    if not args.no_configs:
+        out["configs"] = config_runs(ctx, torch, max(4, args.steps // 2), cpu=not args.no_cpu_baseline)
     if not args.no_dit:
         out["dit_step"] = dit_step(ctx, awa_hip, torch, args.dit_steps, 1)
+        # the AWA layer inside the step: inputs written by the QKV GEMM just before,
+        # outputs read by the out projection (the headline value replays one layer on
+        # resident inputs, whose ~225 MB working set stays in the 256 MB Infinity Cache)
+        out["awa_ms_per_layer_in_dit_step"] = out["dit_step"]["awa_ms_per_layer_in_step"]
+        if not args.no_mlp10240:
+            out["dit_step_mlp10240"] = dit_step(ctx, awa_hip, torch, max(2, args.dit_steps // 2), 1, mlp=10240,
+                                                graph=False)
+            out["dit_step_mlp10240"]["label"] = ("BASELINE config 3 as written (MLP 2560->10240->2560); the "
+                                                 "reference checkpoint's width is 6912 (dit_step)")
     if not args.no_cpu_baseline:
         vqf = vq.float().cpu().numpy()
         tqf = tq.float().cpu().numpy()
