@@ -102,7 +102,7 @@ typedef struct {
 } dit_io_weights;
 
 /* Prepared input/output layers: padded device copies of vid_in_w (K 132 ->
- * 160) and vid_out_w / vid_out_b (N 64 -> 256) for the block's GEMM kernel;
+ * 192) and vid_out_w / vid_out_b (N 64 -> 256) for the block's GEMM kernel;
  * the other pointers are borrowed and must stay valid. */
 typedef struct dit_io dit_io;
 int dit_io_create(awa_ctx* ctx, const dit_io_weights* w, dit_io** out, awa_stream_t stream);

@@ -35,14 +35,14 @@ GemmProblem problem(const uint16_t* A, int lda, const uint16_t* W, int ldw, int 
     return p;
 }
 
-constexpr int VID_IN = 132, VID_IN_PAD = 160;   // patch channels 33 x 2 x 2; K padded to the GEMM step
+constexpr int VID_IN = 132, VID_IN_PAD = 192;   // patch channels 33 x 2 x 2; K padded to the GEMM step (64)
 constexpr int VID_OUT = 64, VID_OUT_PAD = 256;  // output channels 16 x 2 x 2; N padded to the GEMM tile
 
 }  // namespace
 
 struct dit_io {
     int device = 0;
-    uint16_t* vid_in_w = nullptr;   // [2560][160], columns 132.. zero
+    uint16_t* vid_in_w = nullptr;   // [2560][192], columns 132.. zero
     const float* vid_in_b = nullptr;
     const uint16_t* txt_in_w = nullptr;
     const float* txt_in_b = nullptr;
@@ -108,7 +108,7 @@ int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H,
     DeviceGuard dg(ctx->device);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int Lv = T * (H / 2) * (W / 2), M = Lv + TXT;
-    // workspace: patches [Lv][160] bf16 | text [TXT][5120] bf16
+    // workspace: patches [Lv][192] bf16 | text [TXT][5120] bf16
     const size_t o_t = align256((size_t)Lv * VID_IN_PAD * 2);
     HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, o_t + align256((size_t)TXT * 5120 * 2)));
     uint16_t* patch = static_cast<uint16_t*>(ctx->ws);

@@ -7,17 +7,22 @@
 // ends with four consecutive output features of one activation row, which
 // the epilogues store as 8- or 16-byte pieces of row-major outputs.
 //
-// Workgroup tile 256 (n) x 256 (m), K step 32, four wave64 in a 2x2 grid of
+// Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
 // 128x128 wave tiles (16 accumulators per wave).  Operand k-slices reach LDS
-// by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into a 5-stage
-// ring (5 x 32 KiB, all of LDS), four stages in flight; the loop waits on
-// the DMA counter with explicit s_waitcnt and a bare s_barrier (a
-// __syncthreads would drain every outstanding load).  Rows are 64 bytes with
-// a 16-byte-chunk XOR swizzle, chunk ^ ((row >> 2) & 3).  Each k16 sub-step
-// issues its 16 MFMAs with the next sub-step's fragment reads (and the DMA
-// pieces) one after each of the first eight.  Tiles are walked in groups of four
-// m-tiles and assigned to XCDs in contiguous ranges, so the workgroups
-// resident on one XCD share A and W k-slices through its L2.
+// by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into two 64 KiB
+// stages: while one stage is computed the next one lands.  LDS rows are 128
+// bytes (64 k of one operand row), so every DMA instruction reads whole
+// 128-byte segments of global memory: with 64-byte rows (K step 32) the same
+// bytes took twice the L2 requests and measurably longer to arrive.  A
+// 16-byte-chunk XOR swizzle, chunk ^ ((row >> 1) & 7), keeps the fragment
+// reads conflict-free.  The loop waits on the DMA counter with explicit
+// s_waitcnt and a bare s_barrier (a __syncthreads would drain every
+// outstanding load).  Each k16 sub-step issues its 16 MFMAs with the next
+// sub-step's fragment reads one after each of the first eight (and, in the
+// sub-step that refills the freed stage, one DMA piece after each MFMA).
+// Tiles are walked in groups of four m-tiles and assigned to XCDs in
+// contiguous ranges, so the workgroups resident on one XCD share A and W
+// k-slices through its L2.
 //
 // Epilogues (the elementwise tail of each projection in dit_vk.cpp:517-632):
 //   EPI_STORE     C = bf16(acc)                               (qkv)
@@ -36,15 +41,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 typedef __attribute__((address_space(3))) void* lptr_t;
 
-constexpr int BN = 256, BM = 256, BK = 32;
-constexpr int NSTAGE = 5;                 // LDS ring (5 x 32 KiB = all of LDS): four K-steps of DMA in flight
-constexpr int ROW_E = BK;                 // bf16 per LDS row (64 B, 4 chunks)
+constexpr int BN = 256, BM = 256, BK = 64;
+constexpr int NSTAGE = 2;                 // two 64 KiB stages: one computed while the next lands
+constexpr int ROW_E = BK;                 // bf16 per LDS row (128 B, 8 chunks)
 constexpr int STAGE_E = (BN + BM) * ROW_E;
 
-// LDS has 64 four-byte banks (a 256-byte window); a 64-byte row is a quarter
-// of it, so chunk ^ ((row >> 2) & 3) gives the 16 rows read by a quarter-wave
+// LDS has 64 four-byte banks (a 256-byte window); a 128-byte row is half of
+// it, so chunk ^ ((row >> 1) & 7) gives the 16 rows read by a quarter-wave
 // 16 distinct 16-byte bank groups.
-__device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 2) & 3)) << 3); }
+__device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 
 // Epilogues go through LDS so that global memory sees whole rows: stores of
@@ -191,37 +196,37 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
 
     // Operand tiles go straight from global memory into LDS
     // (buffer_load_dwordx4 ... lds: lane i of a wave writes 16 bytes at
-    // M0 + 16 i).  One wave instruction fills 1 KiB = 16 swizzled rows; lane l
-    // lands in row r0 + l/4, physical chunk l%4, so it fetches the logical
-    // chunk that the swizzle maps there.  Each wave issues 4 + 4 per stage.
-    const int lrow = lane >> 2;
+    // M0 + 16 i).  One wave instruction fills 1 KiB = 8 swizzled rows; lane l
+    // lands in row r0 + l/8, physical chunk l%8, so it fetches the logical
+    // chunk that the swizzle maps there.  Each wave issues 8 + 8 per stage.
+    const int lrow = lane >> 3;
     const uint16_t* Wp = p.W + (size_t)n0 * p.ldw;
     // Buffer loads (SGPR resource + 32-bit lane offset + SGPR k offset) issue
     // measurably faster than global loads with 64-bit lane addresses.  Rows
     // of A past M repeat the last row; the resource range bounds every read.
     const uint16_t* Ap = p.A + (size_t)m0 * p.lda;
     const int arows = min(BM, p.M - m0);
-    int woff[4], aoff[4];   // byte offsets of this lane's 16 bytes at k = 0
+    int woff[8], aoff[8];   // byte offsets of this lane's 16 bytes at k = 0
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = (wave * 4 + i) * 16 + lrow;
-        const int lch = (lane & 3) ^ ((row >> 2) & 3);
+    for (int i = 0; i < 8; i++) {
+        const int row = (wave * 8 + i) * 8 + lrow;
+        const int lch = (lane & 7) ^ ((row >> 1) & 7);
         woff[i] = (row * p.ldw + lch * 8) * 2;
         aoff[i] = (min(row, arows - 1) * p.lda + lch * 8) * 2;
     }
     // raw buffer, 32-bit dword format (word 3 of the resource)
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc((void*)Wp, 0, BN * p.ldw * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc((void*)Ap, 0, arows * p.lda * 2, 0x00020000);
-    // piece g (0..7) of stage kt into ring slot `slot`: W block g/2 (even g)
-    // or A block g/2 (odd g), 16 rows of 64 bytes
+    // piece g (0..15) of stage kt into ring slot `slot`: W block g/2 (even g)
+    // or A block g/2 (odd g), 8 rows of 128 bytes
     auto load_piece = [&](int kt, int slot, int g) __attribute__((always_inline)) {
-        uint16_t* dst = lds + slot * STAGE_E + ((g & 1) ? BN * ROW_E : 0) + (wave * 4 + (g >> 1)) * 512;
+        uint16_t* dst = lds + slot * STAGE_E + ((g & 1) ? BN * ROW_E : 0) + (wave * 8 + (g >> 1)) * 512;
         if (g & 1) __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lptr_t)dst, 16, aoff[g >> 1], kt * BK * 2, 0, 0);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lptr_t)dst, 16, woff[g >> 1], kt * BK * 2, 0, 0);
     };
     auto load = [&](int kt, int slot) __attribute__((always_inline)) {
 #pragma unroll
-        for (int g = 0; g < 8; g++) load_piece(kt, slot, g);
+        for (int g = 0; g < 16; g++) load_piece(kt, slot, g);
     };
 
     f32x16 acc[4][4];
@@ -253,11 +258,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     };
     // One k16 sub-step: the 16 MFMAs on fragment buffer `buf`; after each of
     // the first eight, one fragment read of the next sub-step (slot rslot,
-    // sub-step rs, into buffer buf ^ 1) and, when `dma`, one DMA piece of
-    // stage dma_kt.  sched_barrier pins this order: every read is in
-    // flight half a sub-step before its use, the wait for the previous
-    // sub-step's reads comes before the first new read (the compiler waits
-    // on the LDS counter with lgkmcnt(0)), and the DMA issue is spread out.
+    // sub-step rs, into buffer buf ^ 1) and, when `dma`, after each of the
+    // sixteen one DMA piece of stage dma_kt.  sched_barrier pins this order:
+    // every read is in flight half a sub-step before its use, the wait for
+    // the previous sub-step's reads comes before the first new read (the
+    // compiler waits on the LDS counter with lgkmcnt(0)), and the DMA issue
+    // is spread out.
     auto substep = [&](int buf, int rslot, int rs, bool do_read, bool dma, int dma_kt, int dma_slot)
         __attribute__((always_inline)) {
         const uint16_t* ws = lds + rslot * STAGE_E;
@@ -266,8 +272,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
         for (int g = 0; g < 16; g++) {
             const int i = g >> 2, j = g & 3;
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
+            if (dma) load_piece(dma_kt, dma_slot, g);
             if (g < 8) {
-                if (dma) load_piece(dma_kt, dma_slot, g);
                 if (do_read) {
                     const int r = g >> 1;
                     if (g & 1)
@@ -288,28 +294,35 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     // kt+3.  Past the last stage the refill repeats stage nk-1 into the freed
     // slot, which is never read again: the loop body stays branch-free and
     // the DMA count it waits on stays fixed.
+    // Two stages: while stage kt is computed from slot kt & 1, stage kt + 1
+    // lands in the other slot.  Sub-steps 0-2 of stage kt read their
+    // successors' fragments from the same slot; before sub-step 3, every
+    // wave waits for its own DMA of stage kt + 1 and for its LDS reads, and
+    // the barrier then makes stage kt + 1 visible and slot kt & 1 free:
+    // sub-step 3 reads stage kt + 1's first fragments and refills slot kt & 1
+    // with stage kt + 2 (past the last stage it repeats the last stage into
+    // the free slot, so the DMA count stays fixed).
     const int last = nk - 1;
-#pragma unroll
-    for (int s0 = 0; s0 < NSTAGE - 1; s0++) load(min(s0, last), s0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (NSTAGE - 2)) : "memory");
-    // A bare barrier: __syncthreads() would also drain the DMA prefetch.
+    load(0, 0);
+    load(min(1, last), 1);
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, 0);
     int slot = 0;
     for (int kt = 0; kt < last; kt++) {
-        const int nslot = slot == NSTAGE - 1 ? 0 : slot + 1;
         substep(0, slot, 1, true, false, 0, 0);
-        // stage kt+1 landed; stages kt+2 .. kt+NSTAGE-2 may still fly.  The
-        // reads of the slot refilled below (stage kt-1) were consumed by the
-        // MFMAs of the previous step, so no LDS wait is needed here.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (NSTAGE - 3)) : "memory");
+        substep(1, slot, 2, true, false, 0, 0);
+        substep(0, slot, 3, true, false, 0, 0);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        substep(1, nslot, 0, true, true, min(kt + NSTAGE - 1, last), slot == 0 ? NSTAGE - 1 : slot - 1);
-        slot = nslot;
+        substep(1, slot ^ 1, 0, true, true, min(kt + 2, last), slot);
+        slot ^= 1;
     }
     substep(0, slot, 1, true, false, 0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    substep(1, 0, 0, false, false, 0, 0);
+    substep(1, slot, 2, true, false, 0, 0);
+    substep(0, slot, 3, true, false, 0, 0);
+    substep(1, slot, 0, false, false, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the redundant last refill
     // every wave is done with the operand tiles: LDS becomes the staging area
     __syncthreads();
     epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane, lds + wave * (128 * 128));
