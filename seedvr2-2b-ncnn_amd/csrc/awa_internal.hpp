@@ -233,6 +233,7 @@ struct SdpaArgs {
     float scale_log2e;     // multiplier of the scores (1 when Q carries the scale)
 };
 hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s);
+hipError_t launch_sdpa_f32(const SdpaArgs& a, hipStream_t s);   // awa_sdpa_f32.hip
 
 hipError_t launch_coalesce(int dtype, const float* tpart, void* tattn, int nwin, int txt_len,
                            hipStream_t s);

@@ -15,8 +15,10 @@
 // transposed per tile by the pack kernel so that A = V^T is read from LDS with
 // 8-byte loads.
 //
-// bf16 storage -> v_mfma_f32_32x32x16_bf16 (fp32 accumulation).
-// fp32 storage -> v_mfma_f32_32x32x2f32.
+// bf16 storage -> v_mfma_f32_32x32x16_bf16 (fp32 accumulation); fp32
+// storage -> v_mfma_f32_32x32x2f32 in awa_sdpa_f32.hip (a file of its own:
+// this one is compiled with the MFMA accumulators in VGPRs, which the bf16
+// kernel's softmax wants and which made the fp32 kernel spill).
 //
 // Video query rows are scattered back to token order (dit_vk.cpp:445-455);
 // text query rows go to per-window fp32 partials that the coalesce kernel
@@ -43,64 +45,6 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 
-// The key/query tile sequence of one window: its video tiles, then the text
-// tiles of its text set.
-struct WinTiles {
-    int vbase, nvt, tbase, ntt, f, txt;
-    __device__ int tile(int kk) const { return kk < nvt ? vbase + kk : tbase + (kk - nvt); }
-    __device__ int nvalid(int kk) const {
-        return kk < nvt ? min(TILE, f - TILE * kk) : min(TILE, txt - TILE * (kk - nvt));
-    }
-};
-
-__device__ inline WinTiles window_tiles(const SdpaArgs& a, int w) {
-    WinTiles t;
-    t.vbase = a.tile_base[w];
-    t.nvt = a.tile_base[w + 1] - t.vbase;
-    t.ntt = a.ntt;
-    t.tbase = a.n_vid_tiles + (a.txt_sets == 1 ? 0 : w) * a.ntt;
-    t.f = a.cumf[w + 1] - a.cumf[w];
-    t.txt = a.txt_len;
-    return t;
-}
-
-// Hardware dispatches workgroup b to XCD b % 8.  Remap so that each XCD gets
-// a contiguous range of (head, item) ids: consecutive items of one head are
-// mostly the same window and share its K/V tiles through that XCD's L2.
-
-// Online-softmax update of one 64-key tile held as two 32x32 S^T accumulators
-// (lane: query column n = lane % 32; register r: key 8(r/4) + 4(lane/32) + r%4
-// of each 32-key half).  Scales and masks the scores, returns the factor that
-// rescales the running output, and leaves exp2(s - m) in sacc.
-__device__ inline float softmax_tile(f32x16 (&sacc)[2], int kvalid, int hb, float scale,
-                                     float& m_i, float& l_i) {
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = 32 * kt + 8 * (r >> 2) + 4 * hb + (r & 3);
-            const float v = key < kvalid ? sacc[kt][r] * scale : -INFINITY;
-            sacc[kt][r] = v;
-            mloc = fmaxf(mloc, v);
-        }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_i, mloc);  // finite: every tile has a valid key
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(sacc[kt][r] - m_new);
-            sacc[kt][r] = p;
-            psum += p;
-        }
-    l_i = l_i * alpha + psum;
-    m_i = m_new;
-    return alpha;
-}
-
 // Writes the normalised O^T accumulators of one wave (lane: query n, register
 // r of d-tile dt: channel 32dt + 8(r/4) + 4(lane/32) + r%4).
 template <bool kBf16Out>
@@ -122,21 +66,6 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
                     make_float4(o0, o1, o2, o3);
             }
         }
-}
-
-// Destination of query slot `slot` of query tile kq (nullptr: padding slot).
-__device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, int h, int kq,
-                                  int slot, bool& to_text, size_t elem) {
-    if (slot >= wt.nvalid(kq)) return nullptr;
-    if (kq < wt.nvt) {
-        to_text = false;
-        const int g = a.cumf[w] + TILE * kq + slot;
-        const size_t tok = (size_t)a.vidx[g];
-        return reinterpret_cast<char*>(a.vattn) + (tok * DIM + (size_t)h * HEAD_D) * elem;
-    }
-    to_text = true;
-    const int i = TILE * (kq - wt.nvt) + slot;
-    return a.tpart + ((size_t)w * a.txt_len + i) * DIM + (size_t)h * HEAD_D;
 }
 
 // ----------------------------------------------------------------- bf16
@@ -790,147 +719,11 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     }
 }
 
-// ----------------------------------------------------------------- fp32
-constexpr int KP32 = 132;                 // LDS pitch of a K row (floats)
-constexpr int VP32 = 68;                  // LDS pitch of a V^T row (floats)
-constexpr int KS32 = TILE * KP32;
-constexpr int STAGE32 = KS32 + HEAD_D * VP32;
-
-__global__ __launch_bounds__(256, 1) void sdpa_f32_kernel(SdpaArgs a) {
-    __shared__ __align__(16) float lds[2 * STAGE32];
-    const int nblk = a.n_items * HEADS;
-    const int lid = xcd_remap(nblk);
-    if (lid >= nblk) return;
-    const int h = lid / a.n_items;
-    const int item = lid % a.n_items;
-
-    const int4 it = reinterpret_cast<const int4*>(a.items)[item];
-    const int w = it.x;
-    const WinTiles wt = window_tiles(a, w);
-    const int nk = wt.nvt + wt.ntt;
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n = lane & 31, hb = lane >> 5;
-    const int kq = wave < 2 ? it.y : it.z;
-    const bool active = kq >= 0;
-    const int qslot = (wave & 1) * 32 + n;
-
-    const size_t head_off = (size_t)h * a.n_tiles * TILE * HEAD_D;
-    const float* Qh = reinterpret_cast<const float*>(a.Qp) + head_off;
-    const float* Kh = reinterpret_cast<const float*>(a.Kp) + head_off;
-    const float* Vh = reinterpret_cast<const float*>(a.Vp) + head_off;
-
-    // k-step s of S^T pairs channel s (lanes 0-31) with channel 64 + s
-    // (lanes 32-63): lane (n, hb) holds Q[slot][64hb + s].
-    float qf[64];
-    if (active) {
-        const float* qrow = Qh + ((size_t)wt.tile(kq) * TILE + qslot) * HEAD_D + 64 * hb;
-#pragma unroll
-        for (int s = 0; s < 64; s += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(qrow + s);
-            qf[s] = v.x; qf[s + 1] = v.y; qf[s + 2] = v.z; qf[s + 3] = v.w;
-        }
-    }
-
-    float4 kreg[8], vreg[8];
-    auto load_tile = [&](int kk) {
-        const size_t t = (size_t)wt.tile(kk) * TILE * HEAD_D;
-        const float4* ksrc = reinterpret_cast<const float4*>(Kh + t);
-        const float4* vsrc = reinterpret_cast<const float4*>(Vh + t);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            kreg[i] = ksrc[tid + 256 * i];
-            vreg[i] = vsrc[tid + 256 * i];
-        }
-    };
-    auto store_tile = [&](int stage) {
-        float* ks = lds + stage * STAGE32;
-        float* vs = ks + KS32;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<float4*>(ks + (c >> 5) * KP32 + (c & 31) * 4) = kreg[i];
-            *reinterpret_cast<float4*>(vs + (c >> 4) * VP32 + (c & 15) * 4) = vreg[i];
-        }
-    };
-
-    f32x16 oacc[4];
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) oacc[dt][r] = 0.f;
-    float m_i = -INFINITY, l_i = 0.f;
-
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kk = 0; kk < nk; kk++) {
-        const int stage = kk & 1;
-        if (kk + 1 < nk) load_tile(kk + 1);
-        if (active) {
-            const float* ks = lds + stage * STAGE32;
-            const float* vs = ks + KS32;
-            f32x16 sacc[2];
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const float* krow = ks + (32 * kt + n) * KP32 + 64 * hb;
-#pragma unroll
-                for (int s = 0; s < 64; s += 4) {
-                    const float4 kv = *reinterpret_cast<const float4*>(krow + s);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[s], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[s + 1], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[s + 2], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[s + 3], sacc[kt], 0, 0, 0);
-                }
-            }
-            const float alpha = softmax_tile(sacc, wt.nvalid(kk), hb, a.scale_log2e, m_i, l_i);
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) oacc[dt][r] *= alpha;
-            // O^T += V^T P^T; k-step r pairs key 8(r/4)+r%4 (lanes 0-31) with
-            // key 8(r/4)+4+r%4 (lanes 32-63) of the 32-key half kt, which is
-            // exactly where the S^T accumulator left P.
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const float* vrow = vs + (32 * dt + n) * VP32 + 32 * kt + 4 * hb;
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const float4 vv = *reinterpret_cast<const float4*>(vrow + 8 * g);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sacc[kt][4 * g], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sacc[kt][4 * g + 1], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, sacc[kt][4 * g + 2], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, sacc[kt][4 * g + 3], oacc[dt], 0, 0, 0);
-                    }
-                }
-        }
-        if (kk + 1 < nk) store_tile(stage ^ 1);
-        __syncthreads();
-    }
-    if (!active) return;
-    const float l = l_i + __shfl_xor(l_i, 32);
-    const float inv = 1.f / l;
-    bool to_text = false;
-    void* dst = query_dst(a, wt, w, h, kq, qslot, to_text, 4);
-    if (dst == nullptr) return;
-    store_rows<false>(oacc, inv, hb, dst);
-}
-
 }  // namespace
 
 hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s) {
-    const int nblk = a.n_items * HEADS;
-    const int grid = ((nblk + 7) >> 3) << 3;
-    if (dtype == AWA_BF16)
-        hipLaunchKernelGGL(sdpa_bf16_kernel, dim3(a.n_slots), dim3(128), 0, s, a);
-    else
-        hipLaunchKernelGGL(sdpa_f32_kernel, dim3(grid), dim3(256), 0, s, a);
+    if (dtype != AWA_BF16) return launch_sdpa_f32(a, s);
+    hipLaunchKernelGGL(sdpa_bf16_kernel, dim3(a.n_slots), dim3(128), 0, s, a);
     return hipGetLastError();
 }
 
