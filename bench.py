@@ -297,6 +297,38 @@ def dit_step(ctx, awa_hip, torch, steps, warmup, mlp=6912, graph=True):
     return res
 
 
+def gemm_shapes(awa_hip, torch, steps, warmup):
+    """The block's GEMM kernel (plain bf16 store) against hipBLASLt (torch.mm)
+    on the projection shapes of a 1080p layer: M = 5440 + 58 rows; QKV, out,
+    MLP in + gate (fused width 2 x 6912) and MLP out."""
+    ctx = awa_hip.Context(0)
+    dev = torch.device("cuda:0")
+    M = GRID[0] * GRID[1] * GRID[2] + TXT
+    res = {}
+    for name, N, K in (("qkv", 7680, 2560), ("out", 2560, 2560), ("mlp_in", 13824, 2560),
+                       ("mlp_out", 2560, 6912)):
+        g = torch.Generator(device=dev).manual_seed(N + K)
+        A = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+        W = (0.02 * torch.randn((N, K), generator=g, device=dev)).to(torch.bfloat16)
+        C = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+        entry = {"M": M, "N": N, "K": K}
+        for who, fn in (("ours", lambda: ctx.gemm(A, W, out=C)), ("hipblaslt", lambda: torch.mm(A, W.t(), out=C))):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            entry[who] = {"us": round(us, 1), "tflops": round(2.0 * M * N * K / us / 1e6, 1)}
+        res[name] = entry
+    ctx.close()
+    return {"gemm_shapes": res, "unit": "us per GEMM (HIP events, back-to-back launches)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +339,9 @@ def main():
     ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--no-configs", action="store_true", help="skip the 360p fp32, 720p and ragged workloads")
     ap.add_argument("--no-mlp10240", action="store_true", help="skip the MLP-10240 DiT step variant")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="only time the DiT block's GEMM kernel and hipBLASLt (torch.mm) on the four "
+                         "1080p projection shapes (bf16 in and out), print one JSON line and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (4 times) to calibrate the "
                          "FETCH_SIZE/WRITE_SIZE counters, then exit")
@@ -336,6 +371,10 @@ def main():
         return
 
     import awa_hip
+
+    if args.gemm_shapes:
+        print(json.dumps(gemm_shapes(awa_hip, torch, args.steps, args.warmup)))
+        return
 
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(SEED)
