@@ -142,11 +142,11 @@ int awa_forward(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
  * device array of AWA_NOALLOC_SCRATCH_MIB MiB that the library holds on every
  * device it runs on until the process ends (awa_create looks up its address).
  * Geometries whose scratch exceeds it are rejected with AWA_EARG (1080p bf16
- * needs 107 MiB, the 71 x 97 grid with 77 text rows 143 MiB; fp32 storage
- * needs about twice as much).  No per-phase timing events are recorded.  All
- * calls on one device share the array: calls that overlap in time on one
- * device race. */
-enum { AWA_NOALLOC_SCRATCH_MIB = 160 };
+ * needs 76 MiB, the 71 x 97 grid with 77 text rows 104 MiB; fp32 storage
+ * also packs V and needs about 2.6 times as much).  No per-phase timing events
+ * are recorded.  All calls on one device share the array: calls that overlap
+ * in time on one device race. */
+enum { AWA_NOALLOC_SCRATCH_MIB = 128 };
 int awa_forward_noalloc(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
                         const void* d_tqkv, int Lv, int TXT, const float* d_nq_v,
                         const float* d_nk_v, const float* d_nq_t, const float* d_nk_t, float eps,

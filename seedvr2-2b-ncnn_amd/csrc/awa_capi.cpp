@@ -89,7 +89,7 @@ hipError_t dalloc(T** p, size_t n) {
 void free_geom_buffers(awa_geom* g) {
     void* ptrs[] = {g->d_slices, g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win,
                     g->d_items, g->d_sched_start, g->d_sched_desc, g->d_vfreq, g->d_tfreq,
-                    g->d_vcs, g->d_tcs};
+                    g->d_vcs, g->d_tcs, g->d_vrow};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -205,6 +205,13 @@ int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
     if (!P.items.empty())
         HIPCK(ctx, hipMemcpyAsync(g->d_items, P.items.data(), P.items.size() * 4,
                                   hipMemcpyHostToDevice, s));
+    // the bf16 attention kernel's V row table (needs d_cumf and d_vidx); its
+    // 32-bit offsets bound the rows it can address
+    if (P.Lv <= VROW_MAX_ROWS && P.txt_len <= VROW_MAX_ROWS) {
+        HIPCK(ctx, dalloc(&g->d_vrow, (size_t)(P.n_vid_tiles + P.ntt) * TILE));
+        HIPCK(ctx, launch_vrow(g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win, P.n_vid_tiles, P.ntt,
+                               P.txt_len, g->d_vrow, s));
+    }
     return AWA_OK;
 }
 
@@ -285,7 +292,8 @@ namespace awa {
 
 size_t op_scratch_bytes(const GeomPlan& P, int dtype) {
     const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * elem_size(dtype);
-    return 3 * align256(packed) + align256((size_t)P.nwin * P.txt_len * DIM * 4);
+    const size_t n_packed = dtype == AWA_BF16 ? 2 : 3;  // Q, K (and V for fp32)
+    return n_packed * align256(packed) + align256((size_t)P.nwin * P.txt_len * DIM * 4);
 }
 
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
@@ -295,11 +303,13 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     const int Lv = P.Lv;
     const size_t es = elem_size(dtype);
     const size_t packed = (size_t)HEADS * P.n_tiles * TILE * HEAD_D * es;
-    const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = 3 * off_k;
+    const bool bf16 = dtype == AWA_BF16;
+    const size_t off_k = align256(packed), off_v = 2 * off_k, off_t = (bf16 ? 2 : 3) * off_k;
     // the bf16 kernel addresses vattn with 32-bit buffer offsets (and marks
-    // padding rows with offsets from 2^31)
-    if (dtype == AWA_BF16 && (size_t)Lv * DIM * es > 0x7fffffffu) {
-        set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 2 GiB output addressing", Lv);
+    // padding rows with offsets from 2^31), and vqkv / tqkv rows through the
+    // geometry's 32-bit row table
+    if (bf16 && ((size_t)Lv * DIM * es > 0x7fffffffu || !g->d_vrow)) {
+        set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 32-bit addressing", Lv);
         return AWA_EARG;
     }
     char* base = static_cast<char*>(ext_scratch);
@@ -320,7 +330,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     pa.nq_v = d_nq_v; pa.nk_v = d_nk_v; pa.nq_t = d_nq_t; pa.nk_t = d_nk_t;
     pa.cumf = g->d_cumf; pa.vidx = g->d_vidx; pa.tile_base = g->d_tile_base; pa.tile_win = g->d_tile_win;
     pa.vcs = g->d_vcs; pa.tcs = g->d_tcs;
-    pa.Qp = base; pa.Kp = base + off_k; pa.Vp = base + off_v;
+    pa.Qp = base; pa.Kp = base + off_k; pa.Vp = bf16 ? nullptr : base + off_v;
     pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;
     pa.n_tiles = P.n_tiles; pa.eps = eps;
     pa.qscale = (1.0f / std::sqrt(128.0f)) * 1.4426950408889634f;
@@ -329,6 +339,9 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
 
     SdpaArgs sa{};
     sa.Qp = pa.Qp; sa.Kp = pa.Kp; sa.Vp = pa.Vp;
+    sa.vrow = g->d_vrow; sa.vsrc = d_vqkv; sa.tsrc = d_tqkv;
+    sa.vsrc_bytes = (uint32_t)std::min<size_t>((size_t)Lv * QKV * es, 0xffffffffu);
+    sa.tsrc_bytes = (uint32_t)std::min<size_t>((size_t)P.txt_len * QKV * es, 0xffffffffu);
     sa.items = g->d_items; sa.cumf = g->d_cumf; sa.vidx = g->d_vidx; sa.tile_base = g->d_tile_base;
     sa.sched_start = g->d_sched_start; sa.sched_desc = g->d_sched_desc; sa.n_slots = P.n_slots;
     sa.vattn = d_vattn; sa.vattn_bytes = (uint32_t)((size_t)Lv * DIM * es);

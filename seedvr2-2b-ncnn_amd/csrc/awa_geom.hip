@@ -145,7 +145,43 @@ __global__ __launch_bounds__(256) void geom_tables_kernel(const float* __restric
     }
 }
 
+// The V row table of the bf16 attention kernel (layout and clamping in
+// awa_internal.hpp): entry [tile][w][g][j] holds the byte offset of key row
+// 32 w + 4 j + g of the tile in vqkv (video tiles, through vidx) or tqkv.
+__global__ __launch_bounds__(256) void vrow_kernel(const int32_t* __restrict__ cumf,
+                                                   const int32_t* __restrict__ vidx,
+                                                   const int32_t* __restrict__ tile_base,
+                                                   const int32_t* __restrict__ tile_win, int n_vid_tiles,
+                                                   int ntt, int txt_len, uint32_t* __restrict__ vrow) {
+    const long n = (long)(n_vid_tiles + ntt) * TILE;
+    for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (long)gridDim.x * blockDim.x) {
+        const int tile = (int)(e / TILE), pos = (int)(e % TILE);
+        const int R = 32 * (pos >> 5) + 4 * (pos & 7) + ((pos >> 3) & 3);
+        int row;
+        if (tile < n_vid_tiles) {
+            const int w = tile_win[tile];
+            const int f = cumf[w + 1] - cumf[w];
+            row = vidx[cumf[w] + min((tile - tile_base[w]) * TILE + R, f - 1)];
+        } else {
+            row = min((tile - n_vid_tiles) * TILE + R, txt_len - 1);
+        }
+        vrow[e] = (uint32_t)row * (uint32_t)(2 * QKV);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_vrow(const int32_t* cumf, const int32_t* vidx, const int32_t* tile_base,
+                       const int32_t* tile_win, int n_vid_tiles, int ntt, int txt_len, uint32_t* vrow,
+                       hipStream_t s) {
+    const long n = (long)(n_vid_tiles + ntt) * TILE;
+    long blocks = (n + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(vrow_kernel, dim3((unsigned)blocks), dim3(256), 0, s, cumf, vidx, tile_base, tile_win,
+                       n_vid_tiles, ntt, txt_len, vrow);
+    return hipGetLastError();
+}
 
 hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s) {
     int rows = p.sumf > p.nwin * p.txt_len ? p.sumf : p.nwin * p.txt_len;

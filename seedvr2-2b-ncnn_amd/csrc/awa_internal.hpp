@@ -7,13 +7,11 @@
 // Per head h and tile k the packed buffers hold
 //   Qp[h][k][slot 0..63][d 0..127]   normalised + rotated queries
 //   Kp[h][k][slot 0..63][d 0..127]   normalised + rotated keys
-//   Vp[h][k][d 0..127][slot 0..63]   values, transposed inside the tile
+//   Vp[h][k][d 0..127][slot 0..63]   values, transposed inside the tile (fp32 only)
 // in the storage type of the op (bf16 or fp32).  Unused slots are zero.
 // Queries carry the softmax scale times log2(e), so scores come out in log2
-// units.  In bf16 storage the V^T slots of every 16-key group are stored in
-// the order 0-3, 8-11, 4-7, 12-15, which is the order in which the MFMA
-// accumulator of S^T hands the probabilities to the P.V product: a lane's
-// eight V^T values then sit in one 16-byte chunk.
+// units.  The bf16 attention kernel reads V from vqkv / tqkv itself, through
+// the geometry's row table (awa_geom::d_vrow).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -112,6 +110,13 @@ struct GeomPlan {
     std::vector<int32_t> sched_start;  // n_slots+1
     std::vector<int32_t> sched_desc;   // 8 per item, n_items*HEADS items
 };
+// The bf16 kernel's V row table (awa_geom::d_vrow): per V tile (the video
+// tiles, then ntt text tiles shared by all windows) 64 byte offsets of its
+// key rows in vqkv / tqkv (row * 7680 * 2; rows past the end of a window or
+// of the text repeat its last row), stored so that the lane that fetches row
+// 32 w + 4 j + g of the tile (w: wave, g = lane / 16) finds its eight
+// offsets at [tile][w][g][j].  The offsets are 32-bit.
+constexpr long VROW_MAX_ROWS = 0xffffffffL / (2L * QKV);
 
 }  // namespace awa
 
@@ -151,6 +156,7 @@ struct awa_geom {
     float* d_tfreq = nullptr;
     float2* d_vcs = nullptr;   // [sumf][64] (cos, sin) per channel pair, pair 63 = (1, 0)
     float2* d_tcs = nullptr;   // [txt_sets*txt_len][64]
+    uint32_t* d_vrow = nullptr;  // [n_vid_tiles + ntt][64] V row offsets (bf16 attention); nullptr: too many rows
 };
 
 namespace awa {
@@ -192,6 +198,9 @@ void* noalloc_scratch(int device);
 hipError_t launch_geom_build(const GeomParams& p, awa_geom* g, hipStream_t s);
 hipError_t launch_geom_tables(const float* vfreq, const float* tfreq, int sumf, int trows,
                               float2* vcs, float2* tcs, hipStream_t s);
+hipError_t launch_vrow(const int32_t* cumf, const int32_t* vidx, const int32_t* tile_base,
+                       const int32_t* tile_win, int n_vid_tiles, int ntt, int txt_len, uint32_t* vrow,
+                       hipStream_t s);
 
 struct PackArgs {
     const void* vqkv;
@@ -208,7 +217,7 @@ struct PackArgs {
     const float2* tcs;
     void* Qp;
     void* Kp;
-    void* Vp;
+    void* Vp;              // fp32 storage only (the bf16 attention reads V from vqkv / tqkv)
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles;
     float eps;
     float qscale;          // folded into Q: softmax scale 1/sqrt(128) times log2(e)
@@ -218,7 +227,11 @@ hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s);
 struct SdpaArgs {
     const void* Qp;
     const void* Kp;
-    const void* Vp;
+    const void* Vp;              // fp32 kernel
+    const uint32_t* vrow;        // bf16 kernel: V row table of the geometry
+    const void* vsrc;            // bf16 kernel: vqkv and tqkv, whose V columns it reads
+    const void* tsrc;
+    uint32_t vsrc_bytes, tsrc_bytes;
     const int32_t* items;
     const int32_t* cumf;
     const int32_t* vidx;

@@ -7,10 +7,11 @@
 // normalises q and k per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 +
 // eps), y = x / r * g), rotates channel pairs (2i, 2i+1) for i < 63
 // (dit_vk.cpp:62-71; pair 63 of the table is the identity) and writes the
-// packed tiles the SDPA kernel reads: Qp/Kp row-major per tile, Vp transposed
-// per tile (layout in awa_internal.hpp).  HBM-bound: every q, k, v byte is
-// read once and every packed byte written once; all loads of a thread are
-// issued before the first use.
+// packed tiles the SDPA kernel reads: Qp/Kp row-major per tile and, for fp32
+// storage only, Vp transposed per tile (layout in awa_internal.hpp; the bf16
+// attention kernel reads V from vqkv / tqkv itself).  HBM-bound: every byte it
+// needs is read once and every packed byte written once; all loads of a
+// thread are issued before the first use.
 #include "awa_internal.hpp"
 
 namespace awa {
@@ -66,21 +67,19 @@ __device__ inline float row_sum16(float v) {
     return v;
 }
 
-// V staging tile in LDS, [slot][d] with a row pitch of VP 4-byte words.
-// bf16: VP = 65 (odd), so the 16-lane row writes (4-byte stores) of four rows
-// and the transposing column reads below both hit distinct banks;
-// fp32: VP = 129.
-template <typename T> struct VStage;
-template <> struct VStage<uint16_t> { static constexpr int VP = 65; };
-template <> struct VStage<float> { static constexpr int VP = 129; };
+// V staging tile in LDS (fp32), [slot][d] with a row pitch of VP = 129
+// 4-byte words, so that the row writes and the transposing column reads below
+// both hit distinct banks.
+constexpr int VP = 129;
 
 constexpr int RPT = TILE / 16;  // rows per thread (16 rows per 256-thread pass)
 
-template <typename T>
+// kV: also pack V (fp32 storage).
+template <typename T, bool kV>
 __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     using IO = Io<T>;
-    constexpr int VP = VStage<T>::VP;
-    __shared__ uint32_t vs[TILE * VP];
+    static_assert(!kV || sizeof(T) == 4, "V is packed for fp32 storage only");
+    __shared__ uint32_t vs[kV ? TILE * VP : 1];
 
     const int nblk = a.n_tiles * HEADS;
     const int lid = xcd_remap(nblk);
@@ -127,7 +126,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
             const T* row = src + (size_t)(is_txt ? r : vidx[r]) * QKV + col;
             rq[kk] = IO::load(row);
             rk[kk] = IO::load(row + DIM);
-            rv[kk] = IO::load(row + 2 * DIM);
+            if constexpr (kV) rv[kk] = IO::load(row + 2 * DIM);
             const float4* p = cst + ((cs_row0 + r) * CS_STRIDE + c * 4) / 2;
             cs[kk][0] = p[0];
             cs[kk][1] = p[1];
@@ -146,15 +145,14 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     const size_t tile_off = ((size_t)h * a.n_tiles + tile) * TILE * HEAD_D;
     T* Qt = reinterpret_cast<T*>(a.Qp) + tile_off;
     T* Kt = reinterpret_cast<T*>(a.Kp) + tile_off;
-    T* Vt = reinterpret_cast<T*>(a.Vp) + tile_off;
+    T* Vt = kV ? reinterpret_cast<T*>(a.Vp) + tile_off : nullptr;
 
 #pragma unroll
     for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
-        float q[8], k[8], v[8];
+        float q[8], k[8];
         IO::widen(rq[kk], q);
         IO::widen(rk[kk], k);
-        IO::widen(rv[kk], v);
         float sq = 0.f, sk = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -179,54 +177,29 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         }
         IO::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
         IO::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
-        uint32_t* vrow = vs + r * VP;
-        if constexpr (sizeof(T) == 2) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) vrow[c * 4 + i] = bf16_rne(v[2 * i]) | (bf16_rne(v[2 * i + 1]) << 16);
-        } else {
+        if constexpr (kV) {
+            float v[8];
+            IO::widen(rv[kk], v);
+            uint32_t* vrow = vs + r * VP;
 #pragma unroll
             for (int i = 0; i < 8; i++) vrow[c * 8 + i] = __float_as_uint(v[i]);
         }
     }
+    if constexpr (!kV) return;
     __syncthreads();
 
-    // Transposed V tile Vt[d][slot], written as whole 128-byte (bf16) or
-    // 256-byte (fp32) rows by consecutive lanes.
-    if constexpr (sizeof(T) == 2) {
-        // Thread unit (d pair dp, 8-slot chunk sc): eight 4-byte LDS reads give
-        // the chunk for d = 2dp and d = 2dp + 1.  The slots of each 16-slot
-        // group go out in the order 0-3, 8-11, 4-7, 12-15.
+    // Transposed V tile Vt[d][slot] (fp32), written as whole 256-byte rows by
+    // consecutive lanes: thread unit (d, 4-slot chunk sc), 16 chunks per row.
 #pragma unroll
-        for (int it = 0; it < 2; it++) {
-            const int u = it * 256 + tid;
-            const int dp = u >> 3, sc = u & 7;
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                int s0 = sc * 8 + j;
-                const int qd = (s0 >> 2) & 3;
-                if (qd == 1 || qd == 2) s0 ^= 12;
-                const uint32_t w0 = vs[s0 * VP + dp], w1 = vs[(s0 + 1) * VP + dp];
-                lo[j >> 1] = (w0 & 0xffffu) | (w1 << 16);
-                hi[j >> 1] = (w0 >> 16) | (w1 & 0xffff0000u);
-            }
-            uint16_t* dst = reinterpret_cast<uint16_t*>(Vt) + (size_t)(2 * dp) * TILE + sc * 8;
-            *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4*>(dst + TILE) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        }
-    } else {
-        // Thread unit (d, 4-slot chunk sc): 16 chunks per 64-slot row.
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int u = it * 256 + tid;
-            const int d = u >> 4, sc = u & 15;
-            float4 o;
-            o.x = __uint_as_float(vs[(sc * 4 + 0) * VP + d]);
-            o.y = __uint_as_float(vs[(sc * 4 + 1) * VP + d]);
-            o.z = __uint_as_float(vs[(sc * 4 + 2) * VP + d]);
-            o.w = __uint_as_float(vs[(sc * 4 + 3) * VP + d]);
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(Vt) + (size_t)d * TILE + sc * 4) = o;
-        }
+    for (int it = 0; it < 8; it++) {
+        const int u = it * 256 + tid;
+        const int d = u >> 4, sc = u & 15;
+        float4 o;
+        o.x = __uint_as_float(vs[(sc * 4 + 0) * VP + d]);
+        o.y = __uint_as_float(vs[(sc * 4 + 1) * VP + d]);
+        o.z = __uint_as_float(vs[(sc * 4 + 2) * VP + d]);
+        o.w = __uint_as_float(vs[(sc * 4 + 3) * VP + d]);
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(Vt) + (size_t)d * TILE + sc * 4) = o;
     }
 }
 
@@ -235,9 +208,9 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
 hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s) {
     const dim3 grid(xcd_grid((long)a.n_tiles * HEADS)), block(256);
     if (dtype == AWA_BF16)
-        hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, block, 0, s, a);
+        hipLaunchKernelGGL((pack_kernel<uint16_t, false>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL(pack_kernel<float>, grid, block, 0, s, a);
+        hipLaunchKernelGGL((pack_kernel<float, true>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 

@@ -11,9 +11,10 @@
 // formed transposed, S^T = K Q^T, so that a lane owns one query column: the
 // online softmax (exp2, log2(e) folded into the scale) then needs only one
 // cross-lane exchange (lane ^ 32), and the probabilities leave the MFMA
-// accumulator already in the B-operand layout of O^T = V^T P^T.  V is stored
-// transposed per tile by the pack kernel so that A = V^T is read from LDS with
-// 8-byte loads.
+// accumulator already in the B-operand layout of O^T = V^T P^T.  The bf16
+// kernel takes V straight from vqkv / tqkv (no packed copy): its rows are
+// gathered into LDS by DMA and the A operand V^T is read back transposed with
+// ds_read_b64_tr_b16; the fp32 kernel reads a V^T tile packed per window.
 //
 // bf16 storage -> v_mfma_f32_32x32x16_bf16 (fp32 accumulation); fp32
 // storage -> v_mfma_f32_32x32x2f32 in awa_sdpa_f32.hip (a file of its own:
@@ -112,6 +113,8 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 // an 8-pass MFMA).
 typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
+typedef __attribute__((address_space(3))) char lchar_t;
+typedef __attribute__((address_space(3))) bf16x4 lbf16x4_t;
 
 // LDS DMA of one wave's half of a K or V^T tile: eight global_load_lds_dwordx4
 // (lane i writes 16 bytes at M0 + 16 i), instruction j filling the 1 KiB at
@@ -141,28 +144,8 @@ __device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4],
           [m] "s"(m)
         : "memory", "scc", "m0");
 }
-// V^T: instruction j reads global b[j / 2] + vo[j % 2] (b[k] = b0 + 16 k rows
-// of the transposed tile).  No immediate offsets: on these instructions the
-// offset moves the LDS destination as well.
-__device__ inline void dma_v8(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t b3, const uint32_t (&vo)[2],
-                              uint32_t m) {
-    asm volatile(
-        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b1]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b1]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b2]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b2]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b3]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b3]"
-        :
-        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [b0] "s"(b0), [b1] "s"(b1), [b2] "s"(b2), [b3] "s"(b3),
-          [m] "s"(m)
-        : "memory", "scc", "m0");
-}
-// Halves of the above (four instructions, LDS from m), for spreading a tile's
-// DMA between the MFMA slots of a unit: K half h reads base b_h with vo[0..3];
-// V^T half h reads bases ba (vo[0], vo[1]) then bb (vo[0], vo[1]).
+// Half of the above (four instructions, LDS from m): K half h reads base
+// b_h with vo[0..3].
 __device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
     asm volatile(
         "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b]\n\t"
@@ -173,14 +156,18 @@ __device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
         : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b] "s"(b), [m] "s"(m)
         : "memory", "scc", "m0");
 }
-__device__ inline void dma4_v(uint64_t ba, uint64_t bb, const uint32_t (&vo)[2], uint32_t m) {
+// Four V rows-DMA instructions: instruction j fills the 1 KiB at LDS byte
+// address m + 1024 j from byte offset o_j of the buffer r (a head's 256-byte
+// V columns of vqkv or tqkv; an offset outside the buffer reads zeros).
+__device__ inline void dma4_vrow(__amdgpu_buffer_rsrc_t r, uint32_t o0, uint32_t o1, uint32_t o2,
+                                 uint32_t o3, uint32_t m) {
     asm volatile(
-        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[ba]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[ba]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[bb]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[bb]"
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v0], %[r], 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v1], %[r], 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v2], %[r], 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v3], %[r], 0 offen lds"
         :
-        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [ba] "s"(ba), [bb] "s"(bb), [m] "s"(m)
+        : [v0] "v"(o0), [v1] "v"(o1), [v2] "v"(o2), [v3] "v"(o3), [r] "s"(r), [m] "s"(m)
         : "memory", "scc", "m0");
 }
 #pragma clang diagnostic pop
@@ -345,22 +332,40 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // 32 wave + 4 i .. +3; the lane at physical chunk lane % 16 of row
     // 32 wave + 4 i + lane / 16 fetches logical chunk (lane % 16) ^ (row & 15).
     // row & 15 = 4 (i & 3) + lane / 16, so instruction i + 4 is instruction i
-    // shifted by 16 rows.  V^T: instruction i fills rows 64 wave + 8 i .. +7,
-    // logical chunk (lane % 8) ^ ((row >> 1) & 7); instruction i + 2 is
-    // instruction i shifted by 16 rows.
-    uint32_t koff[4], voff[2];  // byte offsets within the tile
+    // shifted by 16 rows.
+    uint32_t koff[4];  // byte offsets within the tile
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = 32 * wave + 4 * i + (lane >> 4);
         koff[i] = 2 * (row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3));
     }
+    // V tiles in LDS: 64 key rows of 256 bytes, the 16-byte chunk c of row r
+    // at physical chunk c ^ vsw(r & 3), vsw = 0, 6, 10, 12.  Instruction j of
+    // wave w fills rows 32 w + 4 j .. +3 (row & 3 = lane / 16), so a lane
+    // always fetches logical chunk (lane % 16) ^ vsw(lane / 16) of its row;
+    // the row's byte offset in the source comes from the geometry's row table
+    // (GeomPlan: vrow), eight per lane and tile.  With this swizzle each group
+    // of 16 (and of 32) lanes of a transposed read below touches distinct banks.
+    auto vsw = [](int r) __attribute__((always_inline)) { return ((r & 1) ? 6 : 0) ^ ((r & 2) ? 10 : 0); };
+    const uint32_t vlane = 16u * (uint32_t)((lane & 15) ^ vsw(lane >> 4));
+    // Transposed reads (ds_read_b64_tr_b16): within each 16-lane group G,
+    // output lane 16 G + 4 a + b receives as element i element b of the 8 bytes
+    // addressed by lane 16 G + 4 i + a.  Read r of fragment (c2, d-tile dt)
+    // of a unit must give lane (n, hb) element i = V[key 16 c2 + 8 r + 4 hb +
+    // i][d 32 dt + n] (the key order of the P^T operand), so lane 16 G + 4 i + a
+    // addresses key row 16 c2 + 8 r + 4 (G >> 1) + i, channels 32 dt +
+    // 16 (G & 1) + 4 a .. +3.  vtr[dt]: that address within a tile for
+    // c2 = r = 0 (byte offset; the unit, c2 and r add multiples of 256).
+    int vtr[4];
+    {
+        const int G = lane >> 4, i = (lane >> 2) & 3, aa = lane & 3;
+        const int x = 2 * (G & 1) + (aa >> 1);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int row = 64 * wave + 8 * i + (lane >> 3);
-        voff[i] = 2 * (row * TILE + (((lane & 7) ^ ((row >> 1) & 7)) << 3));
+        for (int dt = 0; dt < 4; dt++)
+            vtr[dt] = 256 * (4 * (G >> 1) + i) + 16 * ((4 * dt + x) ^ vsw(i)) + 8 * (aa & 1);
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lptr_t)lds;
-    // tile index of key tile kk of work item W
+    // tile index of key tile kk of work item W (packed K)
     auto tile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
         return kk < W.nvt ? W.vbase + kk : W.tbase + (kk - W.nvt);
     };
@@ -369,32 +374,78 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                                                         W.h * head_stride + (size_t)tile_of(W, kk) * KT_E);
         dma_k8(src, src + 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot * KT_E + wave * (KT_E / 2)));
     };
-    auto dma_v = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
-        const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Vp) +
-                                                        W.h * head_stride + (size_t)tile_of(W, kk) * KT_E);
-        dma_v8(src, src + 2 * 16 * TILE, src + 2 * 32 * TILE, src + 2 * 48 * TILE, voff,
-               lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2)));
+    // Row offsets of the next V tile to fetch (vt0: instructions 0-3, vt1:
+    // 4-7), loaded one tile ahead with ordinary loads, so that the compiler
+    // waits for them before any use; vt_ok says whether they are there.
+    // prep_v turns them into this tile's DMA offsets at the start of a tile,
+    // before the tile issues any DMA of its own, so that this wait never
+    // waits for those.
+    u32x4 vt0, vt1;
+    bool vt_ok = false;
+    uint32_t vo[8];
+    auto vtile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
+        return kk < W.nvt ? W.vbase + kk : a.n_vid_tiles + (kk - W.nvt);
     };
-    // Quarter q of the DMA of key tile kk (K half q for q < 2, V^T half q - 2).
-    auto dma_quarter = [&](const Work& W, int q, int kk_k, int slot_k, int kk_v, int slot_v)
-        __attribute__((always_inline)) {
+    auto load_vt = [&](int vtile) __attribute__((always_inline)) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(a.vrow + (size_t)vtile * TILE + wave * 32 + (lane >> 4) * 8);
+        vt0 = p[0];
+        vt1 = p[1];
+    };
+    auto prep_v = [&](const Work& W, int kk) __attribute__((always_inline)) {
+        if (!vt_ok) load_vt(vtile_of(W, kk));
+        vt_ok = true;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            vo[j] = vt0[j] + vlane;
+            vo[4 + j] = vt1[j] + vlane;
+        }
+        asm volatile("" : "+v"(vo[0]), "+v"(vo[1]), "+v"(vo[2]), "+v"(vo[3]), "+v"(vo[4]), "+v"(vo[5]),
+                          "+v"(vo[6]), "+v"(vo[7]));
+    };
+    auto wait_vmem = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    // After the V DMA of key tile kk of W: the row offsets of the next V tile
+    // this slot fetches (tile kk + 1 of W, or tile 0 of the next item Y; when
+    // neither is known, tile kk again, marked as not there).  One load site,
+    // so that the registers need no copies, which would wait for the load.
+    auto after_v = [&](const Work& W, int kk, bool has_y, const Work& Y) __attribute__((always_inline)) {
+        const bool in_w = kk + 1 < W.nvt + a.ntt;
+        vt_ok = in_w || has_y;
+        load_vt(in_w ? vtile_of(W, kk + 1) : has_y ? vtile_of(Y, 0) : vtile_of(W, kk));
+    };
+    // Half h (instructions 4 h .. 4 h + 3) of the V DMA of key tile kk of W
+    // into ring slot `slot` (offsets from prep_v).
+    auto dma_v_half = [&](const Work& W, int kk, int slot, int h) __attribute__((always_inline)) {
+        const bool txt = kk >= W.nvt;
+        const uint32_t col = 2 * (2 * DIM + W.h * HEAD_D);
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(static_cast<const char*>(txt ? a.tsrc : a.vsrc)) + col, 0,
+            (txt ? a.tsrc_bytes : a.vsrc_bytes) - col, 0x00020000);
+        dma4_vrow(r, vo[4 * h], vo[4 * h + 1], vo[4 * h + 2], vo[4 * h + 3],
+                  lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2)) + 4096 * h);
+    };
+    // The whole V DMA of key tile kk of W, then the next offsets.
+    auto dma_v = [&](const Work& W, int kk, int slot, bool has_y, const Work& Y) __attribute__((always_inline)) {
+        dma_v_half(W, kk, slot, 0);
+        dma_v_half(W, kk, slot, 1);
+        after_v(W, kk, has_y, Y);
+    };
+    // Quarter q of the DMA of key tile kk (K half q for q < 2, V half q - 2).
+    auto dma_quarter = [&](const Work& W, int q, int kk_k, int slot_k, int kk_v, int slot_v, bool has_y,
+                           const Work& Y) __attribute__((always_inline)) {
         if (q < 2) {
             const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) +
                                                             W.h * head_stride + (size_t)tile_of(W, kk_k) * KT_E);
             dma4_k(src + q * 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot_k * KT_E + wave * (KT_E / 2)) + 4096 * q);
         } else {
-            const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Vp) +
-                                                            W.h * head_stride + (size_t)tile_of(W, kk_v) * KT_E);
-            const int h = q - 2;
-            dma4_v(src + h * 2 * 32 * TILE, src + h * 2 * 32 * TILE + 2 * 16 * TILE, voff,
-                   lds_base + 2 * ((3 + slot_v) * KT_E + wave * (KT_E / 2)) + 4096 * h);
+            dma_v_half(W, kk_v, slot_v, q - 2);
+            if (q == 3) after_v(W, kk_v, has_y, Y);
         }
     };
-    // The first K tiles and V^T tile of W into ring slots kb, kb + 1 and vb.
-    auto dma_first = [&](const Work& W, int kb, int vb) __attribute__((always_inline)) {
+    // The first K tiles and V tile of W into ring slots kb, kb + 1 and vb.
+    auto dma_first = [&](const Work& W, int kb, int vb, bool has_y, const Work& Y) __attribute__((always_inline)) {
         dma_k(W, 0, kb);
         if (W.nvt + a.ntt > 1) dma_k(W, 1, (kb + 1) % 3);
-        dma_v(W, 0, vb);
+        dma_v(W, 0, vb, has_y, Y);
     };
     // B operand of S^T = K Q^T for column block qb, k-step s:
     // Q[slot 32 qb + n][16 s + 8 hb .. +8]
@@ -434,14 +485,10 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     };
 
     // LDS fragment addresses.  K fragment (k-step s) of a unit: row n of the
-    // unit, chunk 2 s + hb (rows 32 apart share the swizzle).  V^T fragment
-    // (unit half uh, c2, d-tile dt): row 32 dt + n, chunk 4 uh + 2 c2 + hb.
-    // The upper half (uh = 1) flips chunk bit 2, i.e. element-offset bit 5.
-    int kadr[8], vadr[2];
+    // unit, chunk 2 s + hb (rows 32 apart share the swizzle).
+    int kadr[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) kadr[s] = n * HEAD_D + (((2 * s + hb) ^ (n & 15)) << 3);
-#pragma unroll
-    for (int c = 0; c < 2; c++) vadr[c] = n * TILE + (((2 * c + hb) ^ ((n >> 1) & 7)) << 3);
 
     // A fragment of the bias k-step: key column 0 (element 0 of lanes 0-31) = 1.
     bf16x8 ones;
@@ -451,7 +498,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
 
     Work cur = load_work(desc, wi0);
     int kb = 0, vb = 0;  // ring slots of the current item's key tile 0
-    dma_first(cur, kb, vb);
+    prep_v(cur, 0);
+    dma_first(cur, kb, vb, false, cur);
     load_q(cur);
 
     for (int wi = wi0; wi < wi1; wi++) {
@@ -477,7 +525,15 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         float m_i[2] = {0.f, 0.f}, l_i[2] = {0.f, 0.f}, mtc[2] = {0.f, 0.f};
         acc_zero(oacc);
 
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // the query fragments arrive by asm loads: the wait names them, so
+        // nothing reads them before it
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+a"(qf[0][0]), "+a"(qf[0][1]), "+a"(qf[0][2]), "+a"(qf[0][3]),
+                       "+a"(qf[0][4]), "+a"(qf[0][5]), "+a"(qf[0][6]), "+a"(qf[0][7]), "+a"(qf[1][0]),
+                       "+a"(qf[1][1]), "+a"(qf[1][2]), "+a"(qf[1][3]), "+a"(qf[1][4]), "+a"(qf[1][5]),
+                       "+a"(qf[1][6]), "+a"(qf[1][7])
+                     :
+                     : "memory");
         __syncthreads();
 
         // Unit 0: raw scores, m = their row maximum (rounded to bf16), scores
@@ -538,16 +594,24 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     for (int dt = 0; dt < 4; dt++) acc_scale(oacc[qb][dt], alpha[qb]);
                 acc_fence(oacc);
             }
-            // V^T fragments of this unit (loaded once half of the K fragments are dead)
-            const int vofs = (3 + ((vb + (u >> 1)) & 1)) * KT_E;
+            // V^T fragments of this unit (loaded once half of the K fragments
+            // are dead): two transposed reads each, keys 32 (u & 1) + 16 c2 + 8 r.
+            lchar_t* vslot = (lchar_t*)lds + 2 * (3 + ((vb + (u >> 1)) & 1)) * KT_E;
             bf16x8 vf[2][4];
             auto load_vf = [&]() __attribute__((always_inline)) {
 #pragma unroll
-                for (int c2 = 0; c2 < 2; c2++)
+                for (int dt = 0; dt < 4; dt++) {
+                    lchar_t* pv = vslot + vtr[dt];
 #pragma unroll
-                    for (int dt = 0; dt < 4; dt++)
-                        vf[c2][dt] = *reinterpret_cast<const bf16x8*>(
-                            lds + vofs + (vadr[c2] ^ ((u & 1) << 5)) + dt * 32 * TILE);
+                    for (int c2 = 0; c2 < 2; c2++) {
+                        const int row = 32 * (u & 1) + 16 * c2;
+                        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                            (lbf16x4_t*)(pv + 256 * row));
+                        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                            (lbf16x4_t*)(pv + 256 * (row + 8)));
+                        vf[c2][dt] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    }
+                }
             };
             float (&p)[2][16] = scur;  // exponentials in place
             f32x16 snx[2];
@@ -569,8 +633,9 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
                     else qk_only(snx[qb], kf[st], qf[qb][st]);
                     if (j == 3) load_vf();
-                    if ((j == 4 || j == 8) && dk) dma_quarter(cur, j / 8, kk_k, sk, kk_v, sv);
-                    if ((j == 12 || j == 16) && dv) dma_quarter(cur, 2 + (j - 12) / 4, kk_k, sk, kk_v, sv);
+                    if ((j == 4 || j == 8) && dk) dma_quarter(cur, j / 8, kk_k, sk, kk_v, sv, has_next, nxt);
+                    if ((j == 12 || j == 16) && dv)
+                        dma_quarter(cur, 2 + (j - 12) / 4, kk_k, sk, kk_v, sv, has_next, nxt);
                 }
             } else {
                 load_vf();
@@ -627,12 +692,15 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         auto tile = [&](int kk, bool last) __attribute__((always_inline)) {
             const bool dk = kk + 2 < nk, dv = kk + 1 < nk;
             const int sk = (kb + kk + 2) % 3, sv = (vb + kk + 1) & 1;
-            if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1);
+            // this tile's V DMA: tile kk + 1, or the next item's first tile
+            if (dv) prep_v(cur, kk + 1);
+            else if (last && has_next) prep_v(nxt, 0);
+            if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1, false, nxt);
             if (active) {
                 unit(2 * kk, true, dk, dv, kk + 2, sk, kk + 1, sv);
             } else {  // an idle wave still fills its half of the tiles
                 if (dk) dma_k(cur, kk + 2, sk);
-                if (dv) dma_v(cur, kk + 1, sv);
+                if (dv) dma_v(cur, kk + 1, sv, has_next, nxt);
             }
             // the item's last unit computes no scores: Q is dead, so the
             // next item's query tile loads during it (after the slot's last
@@ -640,7 +708,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             if (last) load_q(nxt);
             if (active) unit(2 * kk + 1, !last, false, false, 0, 0, 0, 0);
             if (!last) {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                wait_vmem();
                 __syncthreads();
             }
         };
