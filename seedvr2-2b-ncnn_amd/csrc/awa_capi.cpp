@@ -89,7 +89,7 @@ hipError_t dalloc(T** p, size_t n) {
 void free_geom_buffers(awa_geom* g) {
     void* ptrs[] = {g->d_slices, g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win,
                     g->d_items, g->d_sched_start, g->d_sched_desc, g->d_vfreq, g->d_tfreq,
-                    g->d_vcs, g->d_tcs, g->d_vrow};
+                    g->d_vcs, g->d_tcs, g->d_tile_meta, g->d_vrow};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -110,6 +110,17 @@ void plan_tiles(GeomPlan& P) {
     }
     P.n_vid_tiles = P.tile_base[P.nwin];
     P.n_tiles = P.n_vid_tiles + P.txt_sets * P.ntt;
+    P.tile_meta.clear();
+    for (int w = 0; w < P.nwin; w++)
+        for (int g0 = P.cumf[w]; g0 < P.cumf[w + 1]; g0 += TILE) {
+            P.tile_meta.push_back(g0);
+            P.tile_meta.push_back(std::min(TILE, P.cumf[w + 1] - g0));
+        }
+    for (int set = 0; set < P.txt_sets; set++)
+        for (int j0 = 0; j0 < P.txt_len; j0 += TILE) {
+            P.tile_meta.push_back(set * P.txt_len + j0);
+            P.tile_meta.push_back(std::min(TILE, P.txt_len - j0));
+        }
     P.items.clear();
     for (int w = 0; w < P.nwin; w++) {
         const int nq = (P.tile_base[w + 1] - P.tile_base[w]) + P.ntt;
@@ -205,13 +216,13 @@ int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
     if (!P.items.empty())
         HIPCK(ctx, hipMemcpyAsync(g->d_items, P.items.data(), P.items.size() * 4,
                                   hipMemcpyHostToDevice, s));
-    // the bf16 attention kernel's V row table (needs d_cumf and d_vidx); its
-    // 32-bit offsets bound the rows it can address
-    if (P.Lv <= VROW_MAX_ROWS && P.txt_len <= VROW_MAX_ROWS) {
-        HIPCK(ctx, dalloc(&g->d_vrow, (size_t)(P.n_vid_tiles + P.ntt) * TILE));
-        HIPCK(ctx, launch_vrow(g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win, P.n_vid_tiles, P.ntt,
-                               P.txt_len, g->d_vrow, s));
-    }
+    HIPCK(ctx, dalloc(&g->d_tile_meta, P.tile_meta.size()));
+    HIPCK(ctx, hipMemcpyAsync(g->d_tile_meta, P.tile_meta.data(), P.tile_meta.size() * 4,
+                              hipMemcpyHostToDevice, s));
+    // the row table (needs d_cumf and d_vidx)
+    HIPCK(ctx, dalloc(&g->d_vrow, (size_t)(P.n_vid_tiles + P.ntt) * TILE));
+    HIPCK(ctx, launch_vrow(g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win, P.n_vid_tiles, P.ntt,
+                           P.txt_len, g->d_vrow, s));
     return AWA_OK;
 }
 
@@ -308,7 +319,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     // the bf16 kernel addresses vattn with 32-bit buffer offsets (and marks
     // padding rows with offsets from 2^31), and vqkv / tqkv rows through the
     // geometry's 32-bit row table
-    if (bf16 && ((size_t)Lv * DIM * es > 0x7fffffffu || !g->d_vrow)) {
+    if (bf16 && ((size_t)Lv * DIM * es > 0x7fffffffu || Lv > VROW_MAX_ROWS || P.txt_len > VROW_MAX_ROWS)) {
         set_err(ctx, "awa_forward: Lv=%d video rows exceed the bf16 path's 32-bit addressing", Lv);
         return AWA_EARG;
     }
@@ -328,7 +339,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     PackArgs pa{};
     pa.vqkv = d_vqkv; pa.tqkv = d_tqkv;
     pa.nq_v = d_nq_v; pa.nk_v = d_nk_v; pa.nq_t = d_nq_t; pa.nk_t = d_nk_t;
-    pa.cumf = g->d_cumf; pa.vidx = g->d_vidx; pa.tile_base = g->d_tile_base; pa.tile_win = g->d_tile_win;
+    pa.tile_meta = g->d_tile_meta; pa.vrow = g->d_vrow;
     pa.vcs = g->d_vcs; pa.tcs = g->d_tcs;
     pa.Qp = base; pa.Kp = base + off_k; pa.Vp = bf16 ? nullptr : base + off_v;
     pa.n_vid_tiles = P.n_vid_tiles; pa.ntt = P.ntt; pa.txt_sets = P.txt_sets; pa.txt_len = P.txt_len;

@@ -99,6 +99,7 @@ struct GeomPlan {
     std::vector<int32_t> cumf;       // nwin+1
     std::vector<int32_t> tile_base;  // nwin+1, first video tile of window w
     std::vector<int32_t> tile_win;   // n_vid_tiles, window of each video tile
+    std::vector<int32_t> tile_meta;  // n_tiles*2: RoPE-table row of slot 0, valid rows
     std::vector<int32_t> items;      // n_items*4: window, first q tile, second q tile (-1), 0
     // Persistent schedule of the bf16 attention kernel: one workgroup per
     // resident slot (two per CU); slot s runs on XCD s % 8 and processes the
@@ -110,13 +111,16 @@ struct GeomPlan {
     std::vector<int32_t> sched_start;  // n_slots+1
     std::vector<int32_t> sched_desc;   // 8 per item, n_items*HEADS items
 };
-// The bf16 kernel's V row table (awa_geom::d_vrow): per V tile (the video
-// tiles, then ntt text tiles shared by all windows) 64 byte offsets of its
-// key rows in vqkv / tqkv (row * 7680 * 2; rows past the end of a window or
-// of the text repeat its last row), stored so that the lane that fetches row
-// 32 w + 4 j + g of the tile (w: wave, g = lane / 16) finds its eight
-// offsets at [tile][w][g][j].  The offsets are 32-bit.
+// Row table (awa_geom::d_vrow): per row tile (the video tiles, then ntt
+// text tiles shared by all windows) the 64 row indices of its rows in vqkv
+// (video, through vidx) or tqkv (text); rows past the end of a window or of
+// the text repeat its last row.  Stored so that the lane of the bf16
+// attention kernel that fetches row 32 w + 4 j + g of a tile (w: wave,
+// g = lane / 16) finds its eight rows at [tile][w][g][j]; vrow_pos gives the
+// position of row r.  The attention kernel's byte offsets (row * 7680 * 2)
+// are 32-bit, which bounds the rows of the bf16 path.
 constexpr long VROW_MAX_ROWS = 0xffffffffL / (2L * QKV);
+__host__ __device__ inline int vrow_pos(int r) { return 32 * (r >> 5) + 8 * (r & 3) + ((r & 31) >> 2); }
 
 }  // namespace awa
 
@@ -156,7 +160,8 @@ struct awa_geom {
     float* d_tfreq = nullptr;
     float2* d_vcs = nullptr;   // [sumf][64] (cos, sin) per channel pair, pair 63 = (1, 0)
     float2* d_tcs = nullptr;   // [txt_sets*txt_len][64]
-    uint32_t* d_vrow = nullptr;  // [n_vid_tiles + ntt][64] V row offsets (bf16 attention); nullptr: too many rows
+    int32_t* d_tile_meta = nullptr;  // GeomPlan::tile_meta
+    uint32_t* d_vrow = nullptr;      // [n_vid_tiles + ntt][64] row table (layout above)
 };
 
 namespace awa {
@@ -209,10 +214,8 @@ struct PackArgs {
     const float* nk_v;
     const float* nq_t;
     const float* nk_t;
-    const int32_t* cumf;
-    const int32_t* vidx;
-    const int32_t* tile_base;
-    const int32_t* tile_win;
+    const int32_t* tile_meta;  // GeomPlan::tile_meta
+    const uint32_t* vrow;      // row table
     const float2* vcs;
     const float2* tcs;
     void* Qp;

@@ -3,7 +3,8 @@
 // One workgroup per (64-row tile, head); the 20 heads of a tile are
 // neighbouring work indices on one XCD, so the tile's (cos, sin) rows come
 // from HBM once and from that XCD's L2 for the other heads.  It gathers the
-// tile's rows from vqkv / tqkv (window order through vidx, awa_vk.cpp:73-88),
+// tile's rows from vqkv / tqkv (window order of vidx, awa_vk.cpp:73-88, through
+// the geometry's row table),
 // normalises q and k per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 +
 // eps), y = x / r * g), rotates channel pairs (2i, 2i+1) for i < 63
 // (dit_vk.cpp:62-71; pair 63 of the table is the identity) and writes the
@@ -17,6 +18,9 @@
 namespace awa {
 
 namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T> struct Io;
 
@@ -32,13 +36,12 @@ template <> struct Io<uint16_t> {  // bf16 storage: 8 channels in one 16-byte lo
             x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
         }
     }
+    // round to nearest even, two values per v_cvt_pk_bf16_f32
+    static __device__ inline uint32_t pk(float lo, float hi) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+    }
     static __device__ inline void store8(uint16_t* p, const float* x) {
-        uint4 u;
-        u.x = bf16_rne(x[0]) | (bf16_rne(x[1]) << 16);
-        u.y = bf16_rne(x[2]) | (bf16_rne(x[3]) << 16);
-        u.z = bf16_rne(x[4]) | (bf16_rne(x[5]) << 16);
-        u.w = bf16_rne(x[6]) | (bf16_rne(x[7]) << 16);
-        *reinterpret_cast<uint4*>(p) = u;
+        *reinterpret_cast<uint4*>(p) = make_uint4(pk(x[0], x[1]), pk(x[2], x[3]), pk(x[4], x[5]), pk(x[6], x[7]));
     }
 };
 
@@ -58,13 +61,35 @@ template <> struct Io<float> {
     }
 };
 
-// Sum over the 16 lanes that hold one 128-channel head row.
+// Sum over the 16 lanes that hold one 128-channel head row, a butterfly with
+// DPP lane moves (no LDS round trips): partners lane ^ 1 and lane ^ 2
+// (quad_perm), then the mirror lane in each half of 8 (which holds the other
+// quad's sum) and in the 16 (the other half's): every lane adds the same
+// two partial sums as with partners lane ^ 4 and lane ^ 8, so the result is
+// the xor butterfly's, bit for bit.
+__device__ inline float dpp_add(float v, int ctrl) {
+    int m;
+    switch (ctrl) {  // the control must be a constant
+    case 0xB1: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false); break;  // [1,0,3,2]
+    case 0x4E: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false); break;  // [2,3,0,1]
+    case 0x141: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false); break; // row_half_mirror
+    default: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false); break;    // row_mirror
+    }
+    return v + __int_as_float(m);
+}
 __device__ inline float row_sum16(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
-    return v;
+    v = dpp_add(v, 0xB1);
+    v = dpp_add(v, 0x4E);
+    v = dpp_add(v, 0x141);
+    return dpp_add(v, 0x140);
+}
+// x / r, correctly rounded, from rinv = 1 / r (correctly rounded): q = x rinv
+// is within an ulp of x / r, and one correction step with the exact residual
+// fma(-q, r, x) rounds it correctly (Markstein, IBM J. Res. Dev. 34(1), 1990).
+// Three instructions where the IEEE division takes about ten.
+__device__ inline float div_by(float x, float r, float rinv) {
+    const float q = x * rinv;
+    return __builtin_fmaf(__builtin_fmaf(-q, r, x), rinv, q);
 }
 
 // V staging tile in LDS (fp32), [slot][d] with a row pitch of VP = 129
@@ -90,40 +115,32 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     const int c = tid & 15;     // 8-channel chunk of the head row
     const int r0 = tid >> 4;    // first slot handled by this thread
 
+    // Two levels of loads: the tile's record (RoPE-table row of slot 0,
+    // valid rows) and the thread's row indices from the row table (entries
+    // exist for all 64 rows), then every data load of the thread.
     const bool is_txt = tile >= a.n_vid_tiles;
-    int nvalid;
-    size_t cs_row0;             // table row of slot 0
-    const int32_t* vidx = nullptr;
-    const T* src;
-    if (!is_txt) {
-        const int w = a.tile_win[tile];
-        const int j0 = (tile - a.tile_base[w]) * TILE;
-        const int g0 = a.cumf[w] + j0;
-        nvalid = min(TILE, a.cumf[w + 1] - g0);
-        cs_row0 = g0;
-        vidx = a.vidx + g0;
-        src = reinterpret_cast<const T*>(a.vqkv);
-    } else {
-        const int tt = tile - a.n_vid_tiles;
-        const int set = tt / a.ntt;
-        const int j0 = (tt % a.ntt) * TILE;
-        nvalid = min(TILE, a.txt_len - j0);
-        cs_row0 = (size_t)set * a.txt_len + j0;
-        src = reinterpret_cast<const T*>(a.tqkv) + (size_t)j0 * QKV;
-    }
+    const int2 meta = reinterpret_cast<const int2*>(a.tile_meta)[tile];
+    const uint32_t* rows =
+        a.vrow + (size_t)(is_txt ? a.n_vid_tiles + (tile - a.n_vid_tiles) % a.ntt : tile) * TILE;
+    uint32_t ridx[RPT];
+#pragma unroll
+    for (int kk = 0; kk < RPT; kk++) ridx[kk] = rows[vrow_pos(r0 + 16 * kk)];
+    const int nvalid = meta.y;
+    const size_t cs_row0 = (size_t)meta.x;  // table row of slot 0
+    const T* src = reinterpret_cast<const T*>(is_txt ? a.tqkv : a.vqkv);
     const float4* cst = reinterpret_cast<const float4*>(is_txt ? a.tcs : a.vcs);
     const float* gq = is_txt ? a.nq_t : a.nq_v;
     const float* gk = is_txt ? a.nk_t : a.nk_v;
     const int col = h * HEAD_D + c * 8;
 
-    // Issue every load of the thread: 4 rows x (q, k, v, 4 cos/sin pairs).
+    // Issue every load of the thread: 4 rows x (q, k, [v], 4 cos/sin pairs).
     typename IO::Raw rq[RPT], rk[RPT], rv[RPT];
     float4 cs[RPT][2];
 #pragma unroll
     for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
         if (r < nvalid) {  // uniform across the 16 lanes of a row
-            const T* row = src + (size_t)(is_txt ? r : vidx[r]) * QKV + col;
+            const T* row = src + (size_t)ridx[kk] * QKV + col;
             rq[kk] = IO::load(row);
             rk[kk] = IO::load(row + DIM);
             if constexpr (kV) rv[kk] = IO::load(row + 2 * DIM);
@@ -163,13 +180,16 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         sk = row_sum16(sk);
         const float nq = sqrtf(sq / (float)HEAD_D + a.eps);
         const float nk = sqrtf(sk / (float)HEAD_D + a.eps);
+        const float iq = 1.f / nq, ik = 1.f / nk;
         const float csv[8] = {cs[kk][0].x, cs[kk][0].y, cs[kk][0].z, cs[kk][0].w,
                               cs[kk][1].x, cs[kk][1].y, cs[kk][1].z, cs[kk][1].w};
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const float cn = csv[2 * p], sn = csv[2 * p + 1];
-            const float q0 = q[2 * p] / nq * gqv[2 * p], q1 = q[2 * p + 1] / nq * gqv[2 * p + 1];
-            const float k0 = k[2 * p] / nk * gkv[2 * p], k1 = k[2 * p + 1] / nk * gkv[2 * p + 1];
+            const float q0 = div_by(q[2 * p], nq, iq) * gqv[2 * p];
+            const float q1 = div_by(q[2 * p + 1], nq, iq) * gqv[2 * p + 1];
+            const float k0 = div_by(k[2 * p], nk, ik) * gkv[2 * p];
+            const float k1 = div_by(k[2 * p + 1], nk, ik) * gkv[2 * p + 1];
             q[2 * p] = (q0 * cn - q1 * sn) * a.qscale;
             q[2 * p + 1] = (q1 * cn + q0 * sn) * a.qscale;
             k[2 * p] = k0 * cn - k1 * sn;

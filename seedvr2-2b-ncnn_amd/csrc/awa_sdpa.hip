@@ -232,14 +232,35 @@ __device__ inline void sum_pv(f32x16& o, const bf16x8& v, const bf16x8& p, float
 // bf16 value nearest to x (round to nearest even), as a float.
 __device__ inline float bf16_round(float x) { return __uint_as_float(bf16_rne(x) << 16); }
 // B-operand fragment of the bias k-step: element 0 of lanes 0-31 holds -m of
-// query column n (a bf16 value, so exact), everything else 0.  Paired with
-// the "ones" A fragment (key column 0 = 1), the MFMA adds -m to every score.
+// query column n (a bf16 value, so exact), element 1 holds -2^24, everything
+// else 0.  Paired with the A fragment of mask_frag (key column 0 = 1, key
+// column 1 = 1 for masked keys), the MFMA adds -m to every score and -2^24
+// more to the masked ones, whose exponentials are then 0: no separate
+// masking pass and no branch in the unit loop.
 __device__ inline bf16x8 bias_frag(float m, int hb) {
     bf16x8 b;
 #pragma unroll
     for (int i = 0; i < 8; i++) b[i] = (__bf16)0.f;
-    if (hb == 0) b[0] = (__bf16)(-m);
+    if (hb == 0) {
+        b[0] = (__bf16)(-m);
+        b[1] = (__bf16)(-16777216.f);
+    }
     return b;
+}
+// A-operand fragment of the bias k-step of a unit with kv valid keys (key
+// row n of the unit is masked when n >= kv; kv <= 0 masks all).
+__device__ inline bf16x8 mask_frag(int kv, int n, int hb) {
+    const uint32_t w0 = hb == 0 ? (0x3f80u | (n >= kv ? 0x3f800000u : 0u)) : 0u;
+    const u32x4 w = {w0, 0u, 0u, 0u};
+    return __builtin_bit_cast(bf16x8, w);
+}
+// s[r] -= up for the 16 registers of one column block, in place: the rare
+// rescale path keeps the scores in their registers, so that the common path
+// needs no copies where the two paths meet.
+__device__ inline void sub_inplace(float (&s)[16], float up) {
+    asm volatile("v_sub_f32 %0, %0, %16\n\tv_sub_f32 %1, %1, %16\n\tv_sub_f32 %2, %2, %16\n\tv_sub_f32 %3, %3, %16\n\tv_sub_f32 %4, %4, %16\n\tv_sub_f32 %5, %5, %16\n\tv_sub_f32 %6, %6, %16\n\tv_sub_f32 %7, %7, %16\n\tv_sub_f32 %8, %8, %16\n\tv_sub_f32 %9, %9, %16\n\tv_sub_f32 %10, %10, %16\n\tv_sub_f32 %11, %11, %16\n\tv_sub_f32 %12, %12, %16\n\tv_sub_f32 %13, %13, %16\n\tv_sub_f32 %14, %14, %16\n\tv_sub_f32 %15, %15, %16"
+                 : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]), "+v"(s[6]), "+v"(s[7]), "+v"(s[8]), "+v"(s[9]), "+v"(s[10]), "+v"(s[11]), "+v"(s[12]), "+v"(s[13]), "+v"(s[14]), "+v"(s[15])
+                 : "v"(up));
 }
 
 // Waits after MFMA writes before anything else touches the results (ties the
@@ -344,7 +365,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // wave w fills rows 32 w + 4 j .. +3 (row & 3 = lane / 16), so a lane
     // always fetches logical chunk (lane % 16) ^ vsw(lane / 16) of its row;
     // the row's byte offset in the source comes from the geometry's row table
-    // (GeomPlan: vrow), eight per lane and tile.  With this swizzle each group
+    // (awa_geom::d_vrow), eight per lane and tile.  With this swizzle each group
     // of 16 (and of 32) lanes of a transposed read below touches distinct banks.
     auto vsw = [](int r) __attribute__((always_inline)) { return ((r & 1) ? 6 : 0) ^ ((r & 2) ? 10 : 0); };
     const uint32_t vlane = 16u * (uint32_t)((lane & 15) ^ vsw(lane >> 4));
@@ -396,8 +417,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         vt_ok = true;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            vo[j] = vt0[j] + vlane;
-            vo[4 + j] = vt1[j] + vlane;
+            vo[j] = vt0[j] * (2u * QKV) + vlane;
+            vo[4 + j] = vt1[j] * (2u * QKV) + vlane;
         }
         asm volatile("" : "+v"(vo[0]), "+v"(vo[1]), "+v"(vo[2]), "+v"(vo[3]), "+v"(vo[4]), "+v"(vo[5]),
                           "+v"(vo[6]), "+v"(vo[7]));
@@ -490,12 +511,6 @@ void sdpa_bf16_kernel(SdpaArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; s++) kadr[s] = n * HEAD_D + (((2 * s + hb) ^ (n & 15)) << 3);
 
-    // A fragment of the bias k-step: key column 0 (element 0 of lanes 0-31) = 1.
-    bf16x8 ones;
-#pragma unroll
-    for (int i = 0; i < 8; i++) ones[i] = (__bf16)0.f;
-    if (hb == 0) ones[0] = (__bf16)1.f;
-
     Work cur = load_work(desc, wi0);
     int kb = 0, vb = 0;  // ring slots of the current item's key tile 0
     prep_v(cur, 0);
@@ -584,8 +599,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     m_i[qb] = mn;
                     bfr[qb] = bias_frag(mn, hb);
                     l_i[qb] *= alpha[qb];
-#pragma unroll
-                    for (int r = 0; r < 16; r++) scur[qb][r] -= up;
+                    sub_inplace(scur[qb], up);
                 }
                 acc_fence(oacc);
 #pragma unroll
@@ -620,6 +634,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 // ---- phase A: S(u+1) MFMAs with the exponentials of this unit
                 bf16x8 kf[8];
                 const int ko = k_ofs(u + 1);
+                const bf16x8 onesm = mask_frag(unit_kv(u + 1), n, hb);
 #pragma unroll
                 for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
                 // 18 slots: slot 0 / 1 are the bias k-steps of blocks 0 / 1, slot
@@ -629,7 +644,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 for (int j = 0; j < 18; j++) {
                     const int qb = j & 1, st = (j - 2) >> 1;
                     const int eq = j >> 3, er = 2 * (j & 7);
-                    if (j < 2) exp_qk_first(snx[qb], ones, bfr[qb], p[eq][er], p[eq][er + 1]);
+                    if (j < 2) exp_qk_first(snx[qb], onesm, bfr[qb], p[eq][er], p[eq][er + 1]);
                     else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
                     else qk_only(snx[qb], kf[st], qf[qb][st]);
                     if (j == 3) load_vf();
@@ -655,8 +670,6 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     for (int i = 0; i < 8; i++) pb[qb][c2][i] = (__bf16)p[qb][8 * c2 + i];
             if (has_succ) {
                 mfma_fence_v(snx);
-                const int kvn = unit_kv(u + 1);
-                if (kvn < 32) mask_unit(snx, kvn, hb);
                 // ---- phase B: P.V MFMAs with the row maxima of S(u+1) and the row sums of P(u)
                 float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
