@@ -12,6 +12,13 @@ namespace {
 
 constexpr int CO_BLOCK = 64;  // small blocks: the output is only TXT x 2560
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// two floats -> two bf16, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ inline uint32_t pk_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
 template <bool kBf16Out>
 __global__ __launch_bounds__(CO_BLOCK) void coalesce_kernel(const float* __restrict__ tpart,
                                                             void* __restrict__ out, int nwin, int n4) {
@@ -19,9 +26,19 @@ __global__ __launch_bounds__(CO_BLOCK) void coalesce_kernel(const float* __restr
     if (i >= n4) return;
     const float4* src = reinterpret_cast<const float4*>(tpart) + i;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    // Eight windows' loads in flight at a time; the adds stay in window order.
+    // Sixteen windows' loads in flight at a time (one round trip for up to
+    // 16 windows); the adds stay in window order.
     int w = 0;
-    for (; w + 8 <= nwin; w += 8) {
+    for (; w + 16 <= nwin; w += 16) {
+        float4 v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = src[(size_t)(w + j) * n4];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
+        }
+    }
+    if (w + 8 <= nwin) {
         float4 v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = src[(size_t)(w + j) * n4];
@@ -29,6 +46,7 @@ __global__ __launch_bounds__(CO_BLOCK) void coalesce_kernel(const float* __restr
         for (int j = 0; j < 8; j++) {
             s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
         }
+        w += 8;
     }
     for (; w < nwin; w++) {
         const float4 v = src[(size_t)w * n4];
@@ -38,8 +56,8 @@ __global__ __launch_bounds__(CO_BLOCK) void coalesce_kernel(const float* __restr
     s.x /= fn; s.y /= fn; s.z /= fn; s.w /= fn;
     if constexpr (kBf16Out) {
         uint2 u;
-        u.x = bf16_rne(s.x) | (bf16_rne(s.y) << 16);
-        u.y = bf16_rne(s.z) | (bf16_rne(s.w) << 16);
+        u.x = pk_bf16(s.x, s.y);
+        u.y = pk_bf16(s.z, s.w);
         reinterpret_cast<uint2*>(out)[i] = u;
     } else {
         reinterpret_cast<float4*>(out)[i] = s;

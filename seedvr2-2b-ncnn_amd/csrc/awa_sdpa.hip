@@ -116,59 +116,53 @@ typedef __attribute__((address_space(3))) void* lptr_t;
 typedef __attribute__((address_space(3))) char lchar_t;
 typedef __attribute__((address_space(3))) bf16x4 lbf16x4_t;
 
-// LDS DMA of one wave's half of a K or V^T tile: eight global_load_lds_dwordx4
-// (lane i writes 16 bytes at M0 + 16 i), instruction j filling the 1 KiB at
-// LDS byte address m + 1024 j.  Issued from asm because for the builtin the
-// compiler tracks the pending LDS writes itself: it then drains vmcnt before
-// any LDS store and, since it counts them with the LDS operations, turns every
-// later LDS wait into lgkmcnt(0), so the fragment reads of the score loop and
-// the epilogue's staging round trips could no longer overlap.  The kernel
-// waits for these loads itself (vmcnt(0) and a barrier) before any wave reads
-// the tiles they fill.  M0 written by an SALU instruction needs one wait state
-// before the DMA reads it.
-// K: instruction j reads global b[j / 4] + vo[j % 4] (b1 = b0 + 16 rows).
+// LDS DMA of one wave's half of a K or V tile: eight 16-byte-per-lane loads
+// (lane i writes 16 bytes at M0 + offset + 16 i), instruction j filling the
+// 1 KiB at LDS byte address m + 1024 j.  The instruction offset moves the
+// global address and the LDS destination alike, so four instructions share
+// one M0 write with offsets 0, 1024, 2048, 3072, and each lane's global
+// offset for instruction j is passed with 1024 (j % 4) already subtracted.
+// Issued from asm because for the builtin the compiler tracks the pending LDS
+// writes itself: it then drains vmcnt before any LDS store and, since it
+// counts them with the LDS operations, turns every later LDS wait into
+// lgkmcnt(0), so the fragment reads of the score loop and the epilogue's
+// staging round trips could no longer overlap.  The kernel waits for these
+// loads itself (vmcnt(0) and a barrier) before any wave reads the tiles they
+// fill.  M0 written by an SALU instruction needs one wait state before the
+// DMA reads it.
+// K: four instructions from global base b with lane offsets vo[0..3].
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4], uint32_t m) {
-    asm volatile(
-        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b0]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b1]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b1]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b1]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b1]"
-        :
-        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b0] "s"(b0), [b1] "s"(b1),
-          [m] "s"(m)
-        : "memory", "scc", "m0");
-}
-// Half of the above (four instructions, LDS from m): K half h reads base
-// b_h with vo[0..3].
 __device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
     asm volatile(
-        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], %[b]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], %[b]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], %[b]\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], %[b]"
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %[v0], %[b]\n\t"
+        "global_load_lds_dwordx4 %[v1], %[b] offset:1024\n\t"
+        "global_load_lds_dwordx4 %[v2], %[b] offset:2048\n\t"
+        "global_load_lds_dwordx4 %[v3], %[b] offset:3072"
         :
         : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b] "s"(b), [m] "s"(m)
-        : "memory", "scc", "m0");
+        : "memory", "m0");
 }
-// Four V rows-DMA instructions: instruction j fills the 1 KiB at LDS byte
-// address m + 1024 j from byte offset o_j of the buffer r (a head's 256-byte
-// V columns of vqkv or tqkv; an offset outside the buffer reads zeros).
+// The eight instructions of a wave's K half tile: b1 = b0 + 16 rows.
+__device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4], uint32_t m) {
+    dma4_k(b0, vo, m);
+    dma4_k(b1, vo, m + 4096);
+}
+// V rows: four instructions from buffer r (a head's V columns of vqkv or
+// tqkv, based 3 KiB early so that the compensated offsets stay positive; an
+// offset outside the buffer reads zeros) with lane offsets o_j.
 __device__ inline void dma4_vrow(__amdgpu_buffer_rsrc_t r, uint32_t o0, uint32_t o1, uint32_t o2,
                                  uint32_t o3, uint32_t m) {
     asm volatile(
-        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v0], %[r], 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v1], %[r], 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v2], %[r], 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v3], %[r], 0 offen lds"
+        "s_mov_b32 m0, %[m]\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %[v0], %[r], 0 offen lds\n\t"
+        "buffer_load_dwordx4 %[v1], %[r], 0 offen offset:1024 lds\n\t"
+        "buffer_load_dwordx4 %[v2], %[r], 0 offen offset:2048 lds\n\t"
+        "buffer_load_dwordx4 %[v3], %[r], 0 offen offset:3072 lds"
         :
         : [v0] "v"(o0), [v1] "v"(o1), [v2] "v"(o2), [v3] "v"(o3), [r] "s"(r), [m] "s"(m)
-        : "memory", "scc", "m0");
+        : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -353,12 +347,13 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // 32 wave + 4 i .. +3; the lane at physical chunk lane % 16 of row
     // 32 wave + 4 i + lane / 16 fetches logical chunk (lane % 16) ^ (row & 15).
     // row & 15 = 4 (i & 3) + lane / 16, so instruction i + 4 is instruction i
-    // shifted by 16 rows.
-    uint32_t koff[4];  // byte offsets within the tile
+    // shifted by 16 rows.  koff[i]: the lane's byte offset within the tile
+    // less the instruction offset 1024 i that dma4_k adds.
+    uint32_t koff[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = 32 * wave + 4 * i + (lane >> 4);
-        koff[i] = 2 * (row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3));
+        koff[i] = 2 * (row * HEAD_D + (((lane & 15) ^ (row & 15)) << 3)) - 1024 * i;  // >= 0: row >= 4 i
     }
     // V tiles in LDS: 64 key rows of 256 bytes, the 16-byte chunk c of row r
     // at physical chunk c ^ vsw(r & 3), vsw = 0, 6, 10, 12.  Instruction j of
@@ -417,8 +412,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         vt_ok = true;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            vo[j] = vt0[j] * (2u * QKV) + vlane;
-            vo[4 + j] = vt1[j] * (2u * QKV) + vlane;
+            vo[j] = vt0[j] * (2u * QKV) + vlane + (3072u - 1024u * j);
+            vo[4 + j] = vt1[j] * (2u * QKV) + vlane + (3072u - 1024u * j);
         }
         asm volatile("" : "+v"(vo[0]), "+v"(vo[1]), "+v"(vo[2]), "+v"(vo[3]), "+v"(vo[4]), "+v"(vo[5]),
                           "+v"(vo[6]), "+v"(vo[7]));
@@ -437,7 +432,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // into ring slot `slot` (offsets from prep_v).
     auto dma_v_half = [&](const Work& W, int kk, int slot, int h) __attribute__((always_inline)) {
         const bool txt = kk >= W.nvt;
-        const uint32_t col = 2 * (2 * DIM + W.h * HEAD_D);
+        const uint32_t col = 2 * (2 * DIM + W.h * HEAD_D) - 3072;  // the buffer starts 3 KiB early
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<char*>(static_cast<const char*>(txt ? a.tsrc : a.vsrc)) + col, 0,
             (txt ? a.tsrc_bytes : a.vsrc_bytes) - col, 0x00020000);
