@@ -190,7 +190,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     const int nt = in_group / gm;
     const int n0 = nt * BN, m0 = mt * BM;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // wave is uniform: read into a scalar so that the LDS-DMA destinations
+    // (M0) are formed by scalar instructions, without v_readfirstlane
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wn = wave >> 1, wm = wave & 1;
     const int hb = lane >> 5, r32 = lane & 31;
 
