@@ -2,24 +2,28 @@
 //
 // D = A W^T with A [M][K] (activations, bf16) and W [N][K] (nn.Linear /
 // ncnn InnerProduct layout, bf16); both operands are K-contiguous.  The
-// kernel forms the transposed product per 32x32 block, D^T[n][m] =
-// sum_k W[n][k] A[m][k], with v_mfma_f32_32x32x16_bf16 so that each lane
+// kernel forms the transposed product per 16x16 block, D^T[n][m] =
+// sum_k W[n][k] A[m][k], with v_mfma_f32_16x16x32_bf16 so that each lane
 // ends with four consecutive output features of one activation row, which
-// the epilogues store as 8- or 16-byte pieces of row-major outputs.
+// the epilogues store as 8- or 16-byte pieces of row-major outputs.  The
+// 16x16x32 form does the work of the 32x32x16 one in twice the instructions
+// but draws less power per flop: with all 256 CUs issuing back-to-back MFMAs
+// on random bf16 data the part holds 1.86 GHz with it against 1.65 GHz with
+// 32x32x16 (measured), and a full GEMM here runs at the power limit.
 //
 // Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
-// 128x128 wave tiles (16 accumulators per wave).  Operand k-slices reach LDS
-// by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into two 64 KiB
-// stages: while one stage is computed the next one lands.  LDS rows are 128
-// bytes (64 k of one operand row), so every DMA instruction reads whole
-// 128-byte segments of global memory: with 64-byte rows (K step 32) the same
-// bytes took twice the L2 requests and measurably longer to arrive.  A
+// 128x128 wave tiles (64 accumulators of 16x16 per wave).  Operand k-slices
+// reach LDS by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into two
+// 64 KiB stages: while one stage is computed the next one lands.  LDS rows
+// are 128 bytes (64 k of one operand row), so every DMA instruction reads
+// whole 128-byte segments of global memory: with 64-byte rows (K step 32) the
+// same bytes took twice the L2 requests and measurably longer to arrive.  A
 // 16-byte-chunk XOR swizzle, chunk ^ ((row >> 1) & 7), keeps the fragment
 // reads conflict-free.  The loop waits on the DMA counter with explicit
 // s_waitcnt and a bare s_barrier (a __syncthreads would drain every
-// outstanding load).  Each k16 sub-step issues its 16 MFMAs with the next
-// sub-step's fragment reads one after each of the first eight (and, in the
-// sub-step that refills the freed stage, one DMA piece after each MFMA).
+// outstanding load).  Each k32 sub-step issues its 64 MFMAs with the next
+// sub-step's 16 fragment reads and (in the sub-step that refills the freed
+// stage) 16 DMA pieces interleaved in its first half.
 // Tiles are walked in groups of four m-tiles and assigned to XCDs in
 // contiguous ranges, so the workgroups resident on one XCD share A and W
 // k-slices through its L2.
@@ -37,7 +41,7 @@ namespace awa {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) void* lptr_t;
 
@@ -60,29 +64,26 @@ __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ (
 // conflict-free for both the accumulator-order writes and the row reads) and
 // reads it back row by row, 16 (or 8) lanes per row.
 //
-// Accumulator layout: acc[i][j] is the 32x32 block of output features
-// n_base + 32 i + .. and rows m_base + 32 j + ..; lane (col = lane % 32,
-// hb = lane / 32) holds row 32 j + col, features 32 i + 8 g + 4 hb + t in
-// register 4 g + t.
+// Accumulator layout: acc[i][j] is the 16x16 block of output features
+// n_base + 16 i + .. and rows m_base + 16 j + ..; lane (col = lane % 16,
+// q = lane / 16) holds row 16 j + col, features 16 i + 4 q + t in register t.
 template <int EPI>
-__device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4], int n_base,
+__device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], int n_base,
                                 int m_base, int lane, uint16_t* stg) {
-    const int hb = lane >> 5, col = lane & 31;
+    const int q = lane >> 4, col = lane & 15;
     if constexpr (EPI == EPI_STORE) {
-        // staged rows: 128 features bf16 = 256 bytes, 16 chunks
+        // staged rows: 128 features bf16 = 256 bytes, 16 chunks of 8
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r = 32 * j + col;
+        for (int j = 0; j < 8; j++) {
+            const int r = 16 * j + col;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const f32x16& a = acc[i][j];
-                    const uint2 u = make_uint2(bf16_rne(a[4 * g]) | (bf16_rne(a[4 * g + 1]) << 16),
-                                               bf16_rne(a[4 * g + 2]) | (bf16_rne(a[4 * g + 3]) << 16));
-                    const int c = 4 * i + g;
-                    *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ (r & 15)) << 3) + 4 * hb) = u;
-                }
+            for (int i = 0; i < 8; i++) {
+                const f32x4& a = acc[i][j];
+                const uint2 u = make_uint2(bf16_rne(a[0]) | (bf16_rne(a[1]) << 16),
+                                           bf16_rne(a[2]) | (bf16_rne(a[3]) << 16));
+                const int c = 2 * i + (q >> 1);
+                *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ (r & 15)) << 3) + 4 * (q & 1)) = u;
+            }
         }
         const int c = lane & 15;
         uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + n_base + c * 8;
@@ -93,29 +94,30 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4],
             if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
-        // blocks (0,1) and (2,3): (in, gate) of output features 32 q + ..;
-        // staged rows: 64 features bf16 = 128 bytes, 8 chunks
+        // W rows alternate 32 in / 32 gate: blocks (4h + e, 4h + 2 + e) are
+        // (in, gate) of output features 32 h + 16 e + ..; staged rows: 64
+        // features bf16 = 128 bytes, 8 chunks of 8
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r = 32 * j + col;
+        for (int j = 0; j < 8; j++) {
+            const int r = 16 * j + col;
 #pragma unroll
-            for (int q = 0; q < 2; q++)
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
+                for (int e = 0; e < 2; e++) {
                     uint32_t packed[2];
 #pragma unroll
-                    for (int e = 0; e < 4; e += 2) {
+                    for (int t2 = 0; t2 < 4; t2 += 2) {
                         float o[2];
 #pragma unroll
                         for (int t = 0; t < 2; t++) {
-                            const float h = acc[2 * q][j][4 * g + e + t];
-                            const float gt = acc[2 * q + 1][j][4 * g + e + t];
-                            o[t] = gt / (1.f + __expf(-gt)) * h;
+                            const float hv = acc[4 * h + e][j][t2 + t];
+                            const float gt = acc[4 * h + 2 + e][j][t2 + t];
+                            o[t] = gt / (1.f + __expf(-gt)) * hv;
                         }
-                        packed[e >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
+                        packed[t2 >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
                     }
-                    const int c = 4 * q + g;
-                    *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ (r & 7)) << 3) + 4 * hb) =
+                    const int c = 4 * h + 2 * e + (q >> 1);
+                    *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ (r & 7)) << 3) + 4 * (q & 1)) =
                         make_uint2(packed[0], packed[1]);
                 }
         }
@@ -132,17 +134,15 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x16 (&acc)[4][4],
 #pragma unroll
         for (int half = 0; half < 2; half++) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = 32 * j + col;
+            for (int j = 0; j < 8; j++) {
+                const int r = 16 * j + col;
 #pragma unroll
-                for (int i2 = 0; i2 < 2; i2++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const f32x16& a = acc[2 * half + i2][j];
-                        const int c = 8 * i2 + 2 * g + hb;
-                        *reinterpret_cast<float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2)) =
-                            make_float4(a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
-                    }
+                for (int i2 = 0; i2 < 4; i2++) {
+                    const f32x4& a = acc[4 * half + i2][j];
+                    const int c = 4 * i2 + q;
+                    *reinterpret_cast<float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2)) =
+                        make_float4(a[0], a[1], a[2], a[3]);
+                }
             }
             const int c = lane & 15;
             const int n = n_base + 64 * half + 4 * c;
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     // (M0) are formed by scalar instructions, without v_readfirstlane
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wn = wave >> 1, wm = wave & 1;
-    const int hb = lane >> 5, r32 = lane & 31;
+    const int q = lane >> 4, r16 = lane & 15;
 
     // Operand tiles go straight from global memory into LDS
     // (buffer_load_dwordx4 ... lds: lane i of a wave writes 16 bytes at
@@ -231,79 +231,72 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
         for (int g = 0; g < 16; g++) load_piece(kt, slot, g);
     };
 
-    f32x16 acc[4][4];
+    f32x4 acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+        for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int nk = p.K / BK;
-    int wrow[4], arow[4];
+    int wrow[8], arow[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        wrow[i] = wn * 128 + 32 * i + r32;
-        arow[i] = wm * 128 + 32 * i + r32;
+    for (int i = 0; i < 8; i++) {
+        wrow[i] = wn * 128 + 16 * i + r16;
+        arow[i] = wm * 128 + 16 * i + r16;
     }
-    // fragments of one k16 sub-step: four 32-row blocks of W and of A
-    bf16x8 wf[2][4], af[2][4];
-    // slot `slot`, k16 sub-step s, fragment buffer buf
+    // fragments of one k32 sub-step: eight 16-row blocks of W and of A (lane:
+    // row r16 of the block, k 8 q .. 8 q + 7 of the sub-step)
+    bf16x8 wf[2][8], af[2][8];
+    // slot `slot`, k32 sub-step s, fragment buffer buf
     auto read_frags = [&](int slot, int s, int buf) __attribute__((always_inline)) {
         const uint16_t* ws = lds + slot * STAGE_E;
         const uint16_t* as = ws + BN * ROW_E;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            wf[buf][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 2 * s + hb));
-            af[buf][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 2 * s + hb));
+        for (int i = 0; i < 8; i++) {
+            wf[buf][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 4 * s + q));
+            af[buf][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 4 * s + q));
         }
     };
-    // One k16 sub-step: the 16 MFMAs on fragment buffer `buf`; after each of
-    // the first eight, one fragment read of the next sub-step (slot rslot,
-    // sub-step rs, into buffer buf ^ 1) and, when `dma`, after each of the
-    // sixteen one DMA piece of stage dma_kt.  sched_barrier pins this order:
-    // every read is in flight half a sub-step before its use, the wait for
-    // the previous sub-step's reads comes before the first new read (the
-    // compiler waits on the LDS counter with lgkmcnt(0)), and the DMA issue
-    // is spread out.
+    // One k32 sub-step: the 64 MFMAs on fragment buffer `buf`; in the first
+    // half, after each even one a fragment read of the next sub-step (slot
+    // rslot, sub-step rs, into buffer buf ^ 1) and, when `dma`, after each odd
+    // one a DMA piece of stage dma_kt.  sched_barrier pins this order: every
+    // read is in flight half a sub-step before its use, the wait for the
+    // previous sub-step's reads comes before the first new read (the compiler
+    // waits on the LDS counter with lgkmcnt(0)), and the DMA pieces go out
+    // early, which leaves them a sub-step and a half to land.
     auto substep = [&](int buf, int rslot, int rs, bool do_read, bool dma, int dma_kt, int dma_slot)
         __attribute__((always_inline)) {
         const uint16_t* ws = lds + rslot * STAGE_E;
         const uint16_t* as = ws + BN * ROW_E;
 #pragma unroll
-        for (int g = 0; g < 16; g++) {
-            const int i = g >> 2, j = g & 3;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
-            if (dma) load_piece(dma_kt, dma_slot, g);
-            if (g < 8) {
-                if (do_read) {
-                    const int r = g >> 1;
-                    if (g & 1)
-                        af[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(as + swz(arow[r], 2 * rs + hb));
+        for (int g = 0; g < 64; g++) {
+            const int i = g >> 3, j = g & 7;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (g < 32) {
+                if (dma && (g & 1)) load_piece(dma_kt, dma_slot, g >> 1);
+                if (do_read && !(g & 1)) {
+                    const int r = g >> 2;
+                    if (g & 2)
+                        af[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(as + swz(arow[r], 4 * rs + q));
                     else
-                        wf[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[r], 2 * rs + hb));
+                        wf[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[r], 4 * rs + q));
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Software pipeline over k16 sub-steps: the fragments of the next
-    // sub-step are read beside the 16 MFMAs of the current one.  Between the
-    // two sub-steps of stage kt: wait until stage kt+1 has landed and this
-    // wave's LDS reads are complete, barrier (every wave then has stage kt+1,
-    // and no wave still reads stage kt-1), refill stage kt-1's slot with stage
-    // kt+3.  Past the last stage the refill repeats stage nk-1 into the freed
-    // slot, which is never read again: the loop body stays branch-free and
-    // the DMA count it waits on stays fixed.
-    // Two stages: while stage kt is computed from slot kt & 1, stage kt + 1
-    // lands in the other slot.  Sub-steps 0-2 of stage kt read their
-    // successors' fragments from the same slot; before sub-step 3, every
-    // wave waits for its own DMA of stage kt + 1 and for its LDS reads, and
-    // the barrier then makes stage kt + 1 visible and slot kt & 1 free:
-    // sub-step 3 reads stage kt + 1's first fragments and refills slot kt & 1
-    // with stage kt + 2 (past the last stage it repeats the last stage into
-    // the free slot, so the DMA count stays fixed).
+    // Software pipeline over k32 sub-steps, two per stage, two stages: while
+    // stage kt is computed from slot kt & 1, stage kt + 1 lands in the other
+    // slot.  Sub-step 0 of stage kt reads sub-step 1's fragments from the same
+    // slot; then every wave waits for its own DMA of stage kt + 1 and for its
+    // LDS reads, and the barrier makes stage kt + 1 visible and slot kt & 1
+    // free: sub-step 1 reads stage kt + 1's first fragments and refills slot
+    // kt & 1 with stage kt + 2 (past the last stage it repeats the last stage
+    // into the free slot, so the loop body stays branch-free and the DMA count
+    // it waits on stays fixed).
     const int last = nk - 1;
     load(0, 0);
     load(min(1, last), 1);
@@ -313,16 +306,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     int slot = 0;
     for (int kt = 0; kt < last; kt++) {
         substep(0, slot, 1, true, false, 0, 0);
-        substep(1, slot, 2, true, false, 0, 0);
-        substep(0, slot, 3, true, false, 0, 0);
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         substep(1, slot ^ 1, 0, true, true, min(kt + 2, last), slot);
         slot ^= 1;
     }
     substep(0, slot, 1, true, false, 0, 0);
-    substep(1, slot, 2, true, false, 0, 0);
-    substep(0, slot, 3, true, false, 0, 0);
     substep(1, slot, 0, false, false, 0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the redundant last refill
     // every wave is done with the operand tiles: LDS becomes the staging area
