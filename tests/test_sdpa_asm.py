@@ -1,0 +1,180 @@
+"""Static check of the attention kernel's hand-placed query-fragment loads.
+
+sdpa_bf16_kernel (seedvr2-2b-ncnn_amd/csrc/awa_sdpa.hip) loads the next work
+item's query fragments with inline-asm `global_load_dwordx4 a[..]` straight
+into accumulation registers while the current item finishes, and waits for
+them with the item start's `s_waitcnt vmcnt(0)`.  The compiler does not see
+those loads as loads: if it ever placed a copy or any other use of those
+registers between a load and that wait (a phi copy on a loop edge, a move
+under register pressure), the use would read stale data without any error.
+This test compiles the kernel to AMD assembly with the library's own flags
+(Makefile) and proves on its control-flow graph that on every path from such a
+load no instruction touches the loaded registers before an `s_waitcnt
+vmcnt(0)`.  The analysis is checked on planted mistakes first.
+"""
+import os
+import re
+import shlex
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "seedvr2-2b-ncnn_amd")
+KERNEL = "_ZN3awa12_GLOBAL__N_116sdpa_bf16_kernelENS_8SdpaArgsE"
+HIPCC = "/opt/rocm/bin/hipcc"
+
+AREG = re.compile(r"\ba\[(\d+):(\d+)\]|\ba(\d+)\b")
+LABEL = re.compile(r"^(\.LBB\d+_\d+):")
+VMEM_LOAD = re.compile(r"^(global|buffer|flat)_load_")
+
+
+def makefile_flags():
+    """The library's compile flags for awa_sdpa.hip, as make expands them."""
+    r = subprocess.run(["make", "-n", "-B", "-C", PKG, "_build/awa_sdpa.o"], capture_output=True, text=True,
+                       timeout=60)
+    line = next(l for l in r.stdout.split("\n") if "awa_sdpa.hip" in l and "hipcc" in l)
+    toks = shlex.split(line.split(" -c ")[0])
+    return [t for t in toks[1:] if t != "-fPIC"]
+
+
+def regs(operands):
+    out = set()
+    for m in AREG.finditer(operands):
+        if m.group(3) is not None:
+            out.add(int(m.group(3)))
+        else:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return out
+
+
+def parse(asm_text):
+    """The kernel's instructions as (label or None, opcode, operands) in order."""
+    lines = asm_text.split("\n")
+    start = next(i for i, l in enumerate(lines) if l.startswith(KERNEL + ":"))
+    out = []
+    for l in lines[start + 1:]:
+        if l.startswith(".Lfunc_end"):
+            break
+        m = LABEL.match(l)
+        if m:
+            out.append((m.group(1), None, ""))
+            continue
+        s = l.split(";")[0].strip()
+        if not s or s.startswith("."):
+            continue
+        op, _, rest = s.partition(" ")
+        out.append((None, op, rest.strip()))
+    return out
+
+
+def check(insts):
+    """Returns the violations: (block, instruction, registers) where a
+    register loaded by an AGPR-destination vector load is touched before an
+    s_waitcnt vmcnt(0) on some path, and the number of such loads."""
+    # basic blocks
+    blocks, order = {}, []
+    cur = "entry"
+    blocks[cur] = []
+    order.append(cur)
+    anon = 0
+    for lab, op, rest in insts:
+        if lab is not None:
+            cur = lab
+            blocks[cur] = []
+            order.append(cur)
+            continue
+        blocks[cur].append((op, rest))
+        if op.startswith("s_branch") or op.startswith("s_cbranch") or op == "s_endpgm":
+            anon += 1
+            cur = f"anon{anon}"
+            blocks[cur] = []
+            order.append(cur)
+    succ = {}
+    for i, b in enumerate(order):
+        nxt = order[i + 1] if i + 1 < len(order) else None
+        body = blocks[b]
+        last = body[-1] if body else None
+        s = []
+        if last and last[0] == "s_endpgm":
+            pass
+        elif last and last[0].startswith("s_branch"):
+            s.append(last[1].split()[0])
+        else:
+            if last and last[0].startswith("s_cbranch"):
+                s.append(last[1].split()[0])
+            if nxt is not None:
+                s.append(nxt)
+        succ[b] = [x for x in s if x in blocks]
+    n_loads = sum(1 for b in order for op, rest in blocks[b] if VMEM_LOAD.match(op) and rest.startswith("a"))
+    pend_in = {b: set() for b in order}
+    violations = []
+
+    def run(b, pending, record):
+        pending = set(pending)
+        for op, rest in blocks[b]:
+            if op == "s_waitcnt" and re.search(r"vmcnt\(0\)", rest):
+                pending.clear()
+                continue
+            r = regs(rest)
+            if VMEM_LOAD.match(op) and rest.startswith("a"):
+                pending |= r
+                continue
+            hit = r & pending
+            if hit and record:
+                violations.append((b, f"{op} {rest}", sorted(hit)))
+        return pending
+
+    changed = True
+    while changed:
+        changed = False
+        for b in order:
+            out = run(b, pend_in[b], False)
+            for s in succ[b]:
+                if not out <= pend_in[s]:
+                    pend_in[s] |= out
+                    changed = True
+    for b in order:
+        run(b, pend_in[b], True)
+    return violations, n_loads
+
+
+@pytest.fixture(scope="module")
+def sdpa_asm(tmp_path_factory):
+    if not os.path.exists(HIPCC):
+        pytest.skip("hipcc not present")
+    out = tmp_path_factory.mktemp("asm") / "awa_sdpa.s"
+    cmd = [HIPCC] + makefile_flags() + ["--cuda-device-only", "-S",
+                                        os.path.join(PKG, "csrc", "awa_sdpa.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, cwd=PKG, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return open(out).read()
+
+
+def test_checker_finds_planted_uses(sdpa_asm):
+    insts = parse(sdpa_asm)
+    k = next(i for i, (lab, op, rest) in enumerate(insts)
+             if op and VMEM_LOAD.match(op) and rest.startswith("a"))
+    reg = min(regs(insts[k][2]))
+    # a copy of a loaded register right after the load: found
+    planted = insts[:k + 1] + [(None, "v_accvgpr_read_b32", f"v0, a{reg}")] + insts[k + 1:]
+    v, _ = check(planted)
+    assert any(reg in hit for _, _, hit in v)
+    # the same copy behind a wait: clean
+    waited = insts[:k + 1] + [(None, "s_waitcnt", "vmcnt(0)"), (None, "v_accvgpr_read_b32", f"v0, a{reg}")] + \
+        insts[k + 1:]
+    v2, _ = check(waited)
+    assert not any("v0, a%d" % reg in ins for _, ins, _ in v2)
+    # a use reached only through a branch (the load's block jumps past the
+    # next wait in text order): found through the control-flow graph
+    lab = "_planted"
+    branchy = insts[:k + 1] + [(None, "s_branch", lab), (None, "s_waitcnt", "vmcnt(0)"), (lab, None, ""),
+                               (None, "v_mov_b32", f"v1, a{reg}")] + insts[k + 1:]
+    v3, _ = check(branchy)
+    assert any("v1, a%d" % reg in ins for _, ins, _ in v3)
+
+
+def test_query_fragment_loads_are_waited_for(sdpa_asm):
+    violations, n_loads = check(parse(sdpa_asm))
+    assert n_loads >= 16, "no asm query-fragment loads found: the check would be vacuous"
+    assert not violations, violations[:5]
