@@ -76,7 +76,7 @@ def cpu_baseline(vq_bf16_f32, tq_bf16_f32, gains):
     O.awa_forward(vq_bf16_f32, tq_bf16_f32, g, *gains, eps=1e-5, nthreads=1)
     dt = time.perf_counter() - t0
     # the same restatement parallel over (window, head) on the host cores
-    # (capped at 16, the CPU share of a one-GPU box)
+    # (at most 16 threads: the host cores a single GPU's job gets)
     nt = max(1, min(16, os.cpu_count() or 1))
     t0 = time.perf_counter()
     O.awa_forward(vq_bf16_f32, tq_bf16_f32, g, *gains, eps=1e-5, nthreads=nt)

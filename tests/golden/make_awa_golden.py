@@ -6,7 +6,8 @@ stores its outputs.  The q/k/v projection is an exact map (q = x,
 k = x[:, perm], v = 2 * x[:, ::-1], all products with 0, 1 or 2), so the test
 can rebuild the same vqkv from the seed without storing it, and the
 out-projection is the identity, so the stored rows are the raw attention
-outputs.  Run in the build container (the reference is not on the GPU box):
+outputs.  Run where the reference sources are (the tests only read the
+stored fixture):
 
     python tests/golden/make_awa_golden.py
 """
