@@ -74,7 +74,10 @@ int dit_time_embedding(awa_ctx* ctx, float t, const float* d_w_in, const float* 
  * (unshifted on even layers, shifted on odd ones, dit_vk.cpp:518).  vb / tb
  * are the video and text branches (the same pointer for shared layers).
  * d_emb is the timestep embedding [15360].  mlp is the SwiGLU width (6912 in
- * the reference checkpoint).  Scratch comes from the context. */
+ * the reference checkpoint).  Scratch comes from the context: its workspace
+ * grows (hipMalloc) on the first call with a larger shape, so a caller that
+ * captures this call into a graph runs it once eagerly at that shape first
+ * (dit_graph_create does). */
 int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb,
                       const dit_branch* tb, const float* d_emb, int mlp, int txt_vid_only,
                       float eps, float* d_x, int Lv, int TXT, awa_stream_t stream);
