@@ -148,6 +148,35 @@ def test_bf16_configs(oracle, ctx, name, shifted):
         assert cos >= BF16_COS, cos
 
 
+@pytest.mark.parametrize("txt", [1, 63, 64, 65, 130])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_text_lengths(oracle, ctx, txt, dtype):
+    """Text lengths around the 64-row tile: one row, a tile less one, exactly
+    one tile, one row into a second tile, three tiles (the text keys of a
+    window then span several key tiles, and the text queries several query
+    tiles), shifted 1x12x20 windows (1,2,2)."""
+    torch, _ = torch_dev()
+    grid, nw = (1, 12, 20), (1, 2, 2)
+    note(f"text length {txt} {dtype}")
+    vq, tq, gains = seeded_awa_inputs(grid[0] * grid[1] * grid[2], txt, 40 + txt)
+    o = oracle.Geometry(*grid, nw, txt, 1)
+    geom = ctx.build_geometry(*grid, nw, txt, 1)
+    if dtype == "bf16":
+        rv, rt = bf16_reference(oracle, vq, tq, gains, o)
+        va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.bfloat16)
+    else:
+        rv, rt = oracle.awa_forward(vq, tq, o, *gains, eps=1e-5)
+        va, ta = run_gpu(ctx, geom, vq, tq, gains, torch.float32)
+    for out, ref in ((va, rv), (ta, rt)):
+        cos, rel, md = metrics(out, ref)
+        note(f"  cos={cos:.8f} rel={rel:.2e}")
+        assert np.all(np.isfinite(out))
+        if dtype == "bf16":
+            assert cos >= BF16_COS, cos
+        else:
+            assert cos >= F32_COS and rel <= F32_REL, (cos, rel)
+
+
 def test_f32_on_bf16_config_shapes(oracle, ctx):
     """The fp32 path at the 1080p shifted shape (25 ragged windows)."""
     torch, _ = torch_dev()
