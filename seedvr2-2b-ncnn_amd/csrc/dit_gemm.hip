@@ -60,9 +60,10 @@ __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ (
 // 8- or 16-byte pieces of 32 rows per instruction (the accumulator layout)
 // cost the memory system several times what whole 128-byte lines do.  Each
 // wave stages its 128 x 128 block in its own 32 KiB of LDS as rows of the
-// output (16-byte chunk c of staged row r at chunk c ^ (r & (chunks - 1)),
-// conflict-free for both the accumulator-order writes and the row reads) and
-// reads it back row by row, 16 (or 8) lanes per row.
+// output (16-byte chunk c of staged row r at chunk c ^ (r & 15) for rows of
+// 16 chunks, c ^ ((r >> 1) & 7) for rows of 8, two of which share a 256-byte
+// bank window: conflict-free for both the accumulator-order writes and the
+// row reads) and reads it back row by row, 16 (or 8) lanes per row.
 //
 // Accumulator layout: acc[i][j] is the 16x16 block of output features
 // n_base + 16 i + .. and rows m_base + 16 j + ..; lane (col = lane % 16,
@@ -117,7 +118,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
                         packed[t2 >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
                     }
                     const int c = 4 * h + 2 * e + (q >> 1);
-                    *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ (r & 7)) << 3) + 4 * (q & 1)) =
+                    *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3) + 4 * (q & 1)) =
                         make_uint2(packed[0], packed[1]);
                 }
         }
@@ -126,7 +127,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
 #pragma unroll 8
         for (int it = 0; it < 16; it++) {
             const int r = 8 * it + (lane >> 3), m = m_base + r;
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 64 + ((c ^ (r & 7)) << 3));
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3));
             if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
         }
     } else {  // EPI_RESID, in two halves of 64 features (staged fp32 rows: 256 bytes)
