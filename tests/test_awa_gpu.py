@@ -30,6 +30,8 @@ CONFIGS = {
     # several latent frames: temporal RoPE positions and windows across frames
     "cfg5_frames": ((5, 23, 27), (4, 3, 3), 58, 5, 0.0),
     "cfg6_frames": ((9, 8, 10), (2, 2, 3), 30, 6, 0.0),
+    # three latent frames at the 720p latent grid (7,155 video rows)
+    "cfg7_frames_720p": ((3, 45, 53), (4, 3, 3), 58, 7, 0.0),
 }
 
 
@@ -130,7 +132,8 @@ def bf16_reference(oracle, vq, tq, gains, geom_o):
     return oracle.bf16_round(rv), oracle.bf16_round(rt)
 
 
-@pytest.mark.parametrize("name", ["cfg1_720p", "cfg2_1080p", "cfg4_ragged", "cfg0_360p", "cfg5_frames", "cfg6_frames"])
+@pytest.mark.parametrize("name", ["cfg1_720p", "cfg2_1080p", "cfg4_ragged", "cfg0_360p", "cfg5_frames", "cfg6_frames",
+                                  "cfg7_frames_720p"])
 @pytest.mark.parametrize("shifted", [0, 1])
 def test_bf16_configs(oracle, ctx, name, shifted):
     torch, _ = torch_dev()
