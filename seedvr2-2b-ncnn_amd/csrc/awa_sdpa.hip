@@ -95,11 +95,16 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 //   B(u)  MFMA  O^T += V^T(u) P^T(u)            (16 MFMAs)
 //         VALU  row maximum of S(u+1), row sums of P(u)
 //
-// each MFMA and its share of VALU work issued by one asm statement so that
-// the compiler keeps them together.  The output accumulators O^T (128 AGPRs)
-// and the query fragments (64 AGPRs, the B operand of the score MFMAs) are
-// pinned to the accumulation registers by the asm constraints; the scores
-// live in VGPRs.  The running maximum m stays stale until a unit's
+// Phase A is written with the compiler's MFMA and exp2 builtins, ordered two
+// exponentials then one MFMA by sched_group_barrier, and the scores live in
+// two register sets that alternate between units (unit u exponentiates set
+// u & 1 in place while its MFMAs fill the other): with asm statements naming
+// single score registers the compiler copied all 32 of them at every unit
+// boundary.  Phase B issues each MFMA and its share of VALU work from one asm
+// statement.  The output accumulators O^T (128 AGPRs) and the query fragments
+// (64 AGPRs, the B operand of the score MFMAs) are pinned to the accumulation
+// registers by asm constraints; the scores live in VGPRs.  The running
+// maximum m stays stale until a unit's
 // maximum exceeds it by more than 2^8 (the output is divided by the matching
 // sum at the end, so the result is unchanged); then O^T, the running sum and
 // the pending scores are rescaled.  The upper 32-key half of a short last tile
@@ -107,10 +112,9 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 //
 // Hazards the compiler cannot see through asm: every asm statement issues its
 // VALU work before its MFMA, which supplies the two wait states an MFMA needs
-// after a VALU write of its operands and keeps v_exp_f32 results from being
-// read by the next instruction (transcendental forwarding); explicit waits of
-// sixteen or more cover VALU reads of MFMA results (eleven are required after
-// an 8-pass MFMA).
+// after a VALU write of its operands; explicit waits of sixteen or more cover
+// VALU reads of the results of asm MFMAs (eleven are required after an 8-pass
+// MFMA).  Around the builtins the compiler places the waits itself.
 typedef __attribute__((address_space(1))) void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 typedef __attribute__((address_space(3))) char lchar_t;
@@ -179,32 +183,13 @@ __device__ inline float sum_pair(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Phase A slot: x0, x1 = exp2(x0, x1) in place, then s += k q^T.  The VALU
-// instructions come first, so that they supply the two wait states an MFMA
-// needs after a VALU write of its operands, and nothing reads an exponential
-// in the instruction right after it.
-__device__ inline void exp_qk(f32x16& s, const bf16x8& k, const bf16x8& q, float& x0, float& x1) {
-    asm volatile(
-        "v_exp_f32 %1, %1\n\tv_exp_f32 %2, %2\n\t"
-        "v_mfma_f32_32x32x16_bf16 %0, %3, %4, %0"
-        : "+v"(s), "+v"(x0), "+v"(x1)
-        : "v"(k), "a"(q));
-}
-// A slot without exponentials: s += k q^T.
+// Unit 0's score MFMAs: s += k q^T.
 __device__ inline void qk_only(f32x16& s, const bf16x8& k, const bf16x8& q) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(s) : "v"(k), "a"(q));
 }
 // First MFMA of a chain without exponentials: s = k q^T.
 __device__ inline void qk_zero(f32x16& s, const bf16x8& k, const bf16x8& q) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(s) : "v"(k), "a"(q));
-}
-// First MFMA of a score chain: s = k q^T (accumulator from the constant 0).
-__device__ inline void exp_qk_first(f32x16& s, const bf16x8& k, const bf16x8& q, float& x0, float& x1) {
-    asm volatile(
-        "v_exp_f32 %1, %1\n\tv_exp_f32 %2, %2\n\t"
-        "v_mfma_f32_32x32x16_bf16 %0, %3, %4, 0"
-        : "=&v"(s), "+v"(x0), "+v"(x1)
-        : "v"(k), "v"(q));
 }
 // Phase B slot: mx = max(mx, y0, y1), ps += x0 + x1, then o += v p^T.
 __device__ inline void max_sum_pv(f32x16& o, const bf16x8& v, const bf16x8& p, float& mx, float y0,
@@ -248,15 +233,6 @@ __device__ inline bf16x8 mask_frag(int kv, int n, int hb) {
     const u32x4 w = {w0, 0u, 0u, 0u};
     return __builtin_bit_cast(bf16x8, w);
 }
-// s[r] -= up for the 16 registers of one column block, in place: the rare
-// rescale path keeps the scores in their registers, so that the common path
-// needs no copies where the two paths meet.
-__device__ inline void sub_inplace(float (&s)[16], float up) {
-    asm volatile("v_sub_f32 %0, %0, %16\n\tv_sub_f32 %1, %1, %16\n\tv_sub_f32 %2, %2, %16\n\tv_sub_f32 %3, %3, %16\n\tv_sub_f32 %4, %4, %16\n\tv_sub_f32 %5, %5, %16\n\tv_sub_f32 %6, %6, %16\n\tv_sub_f32 %7, %7, %16\n\tv_sub_f32 %8, %8, %16\n\tv_sub_f32 %9, %9, %16\n\tv_sub_f32 %10, %10, %16\n\tv_sub_f32 %11, %11, %16\n\tv_sub_f32 %12, %12, %16\n\tv_sub_f32 %13, %13, %16\n\tv_sub_f32 %14, %14, %16\n\tv_sub_f32 %15, %15, %16"
-                 : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]), "+v"(s[6]), "+v"(s[7]), "+v"(s[8]), "+v"(s[9]), "+v"(s[10]), "+v"(s[11]), "+v"(s[12]), "+v"(s[13]), "+v"(s[14]), "+v"(s[15])
-                 : "v"(up));
-}
-
 // Waits after MFMA writes before anything else touches the results (ties the
 // registers so that nothing is scheduled across).
 __device__ inline void mfma_fence_v(f32x16 (&s)[2]) {
@@ -530,7 +506,9 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         };
 
         f32x16 oacc[2][4];
-        float scur[2][16];  // scores of the current unit relative to m (later exponentials)
+        // scores relative to m of the current unit (later its exponentials) and
+        // of the next one: unit u reads sc[u & 1] and writes sc[(u + 1) & 1]
+        f32x16 sc[2][2];
         bf16x8 bfr[2];      // bias fragments (-m)
         float m_i[2] = {0.f, 0.f}, l_i[2] = {0.f, 0.f}, mtc[2] = {0.f, 0.f};
         acc_zero(oacc);
@@ -572,7 +550,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 m_i[qb] = bf16_round(max_pair(mx));  // finite: unit 0 has a valid key
                 bfr[qb] = bias_frag(m_i[qb], hb);
 #pragma unroll
-                for (int r = 0; r < 16; r++) scur[qb][r] = s0[qb][r] - m_i[qb];
+                for (int r = 0; r < 16; r++) sc[0][qb][r] = s0[qb][r] - m_i[qb];
             }
         }
 
@@ -594,7 +572,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     m_i[qb] = mn;
                     bfr[qb] = bias_frag(mn, hb);
                     l_i[qb] *= alpha[qb];
-                    sub_inplace(scur[qb], up);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) sc[u & 1][qb][r] -= up;
                 }
                 acc_fence(oacc);
 #pragma unroll
@@ -622,8 +601,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     }
                 }
             };
-            float (&p)[2][16] = scur;  // exponentials in place
-            f32x16 snx[2];
+            f32x16 (&p)[2] = sc[u & 1];  // exponentials in place
+            f32x16 (&snx)[2] = sc[(u + 1) & 1];
             float ps[2] = {0.f, 0.f};
             if (has_succ) {
                 // ---- phase A: S(u+1) MFMAs with the exponentials of this unit
@@ -632,6 +611,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 const bf16x8 onesm = mask_frag(unit_kv(u + 1), n, hb);
 #pragma unroll
                 for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the eight K fragment reads first
                 // 18 slots: slot 0 / 1 are the bias k-steps of blocks 0 / 1, slot
                 // j >= 2 k-step (j - 2) / 2 of block j & 1; exponentials two per
                 // slot, block 0 in slots 0-7, block 1 in slots 8-15.
@@ -639,9 +619,16 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 for (int j = 0; j < 18; j++) {
                     const int qb = j & 1, st = (j - 2) >> 1;
                     const int eq = j >> 3, er = 2 * (j & 7);
-                    if (j < 2) exp_qk_first(snx[qb], onesm, bfr[qb], p[eq][er], p[eq][er + 1]);
-                    else if (j < 16) exp_qk(snx[qb], kf[st], qf[qb][st], p[eq][er], p[eq][er + 1]);
-                    else qk_only(snx[qb], kf[st], qf[qb][st]);
+                    if (j < 16) {
+                        p[eq][er] = __builtin_amdgcn_exp2f(p[eq][er]);
+                        p[eq][er + 1] = __builtin_amdgcn_exp2f(p[eq][er + 1]);
+                    }
+                    if (j < 2)
+                        snx[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(onesm, bfr[qb], f32x16{}, 0, 0, 0);
+                    else
+                        snx[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[qb][st], snx[qb], 0, 0, 0);
+                    if (j < 16) __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     if (j == 3) load_vf();
                     if ((j == 4 || j == 8) && dk) dma_quarter(cur, j / 8, kk_k, sk, kk_v, sv, has_next, nxt);
                     if ((j == 12 || j == 16) && dv)
@@ -664,7 +651,6 @@ void sdpa_bf16_kernel(SdpaArgs a) {
 #pragma unroll
                     for (int i = 0; i < 8; i++) pb[qb][c2][i] = (__bf16)p[qb][8 * c2 + i];
             if (has_succ) {
-                mfma_fence_v(snx);
                 // ---- phase B: P.V MFMAs with the row maxima of S(u+1) and the row sums of P(u)
                 float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
@@ -676,10 +662,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 }
                 mtc[0] = max_pair(mx[0]);
                 mtc[1] = max_pair(mx[1]);
-#pragma unroll
-                for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) scur[qb][r] = snx[qb][r];
+
             } else {
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
