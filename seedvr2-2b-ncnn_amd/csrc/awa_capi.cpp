@@ -136,18 +136,20 @@ void plan_tiles(GeomPlan& P) {
 
 // Static longest-processing-time schedule of the persistent bf16 attention
 // kernel over n_slots resident workgroups.  A work item costs about its
-// window's key-tile count plus one tile for the prologue (Q load, first DMA).
-// All items of one (window, head) go to one XCD so that they share that
-// window's K/V tiles through the XCD's L2; groups are spread over the XCDs
-// longest first onto the least loaded XCD, then each XCD's items onto its
-// slots the same way.  Slot s is workgroup s, dispatched to XCD s % 8.
+// window's key-tile count plus two and a half tiles of per-item work (first
+// scores, the wait for the query tile, the epilogue), as timed per wave on
+// 1080p layers.  All items of one (window, head) go to one XCD so that they
+// share that window's K/V tiles through the XCD's L2; groups are spread over
+// the XCDs longest first onto the least loaded XCD, then each XCD's items onto
+// its slots the same way, or by first fit decreasing when that packs them
+// under a smaller makespan.  Slot s is workgroup s, dispatched to XCD s % 8.
 void plan_schedule(GeomPlan& P, int n_slots) {
     constexpr int XCDS = 8;
     n_slots = std::max(XCDS, n_slots - n_slots % XCDS);
     P.n_slots = n_slots;
     const int per_xcd = n_slots / XCDS;
     std::vector<int> win_cost(P.nwin);
-    for (int w = 0; w < P.nwin; w++) win_cost[w] = 10 * (P.tile_base[w + 1] - P.tile_base[w] + P.ntt) + 12;
+    for (int w = 0; w < P.nwin; w++) win_cost[w] = 10 * (P.tile_base[w + 1] - P.tile_base[w] + P.ntt) + 25;
     struct Group { long cost; int h, w; };
     std::vector<Group> groups;
     std::vector<std::vector<int>> items_of(P.nwin);
@@ -164,17 +166,50 @@ void plan_schedule(GeomPlan& P, int n_slots) {
         for (int i : items_of[gr.w]) xwork[x].push_back(gr.h * P.n_items + i);
     }
     std::vector<std::vector<int>> slot_work(n_slots);
+    auto cost = [&](int id) { return (long)win_cost[P.items[4 * (id % P.n_items)]]; };
     for (int x = 0; x < XCDS; x++) {
         auto& wl = xwork[x];
-        std::stable_sort(wl.begin(), wl.end(), [&](int a, int b) {
-            return win_cost[P.items[4 * (a % P.n_items)]] > win_cost[P.items[4 * (b % P.n_items)]];
-        });
+        std::stable_sort(wl.begin(), wl.end(), [&](int a, int b) { return cost(a) > cost(b); });
+        // longest first onto the least loaded slot
+        std::vector<std::vector<int>> best(per_xcd);
         std::vector<long> sload(per_xcd, 0);
+        long total = 0, cmax = 0;
         for (int id : wl) {
             const int k = (int)(std::min_element(sload.begin(), sload.end()) - sload.begin());
-            sload[k] += win_cost[P.items[4 * (id % P.n_items)]];
-            slot_work[x + XCDS * k].push_back(id);
+            sload[k] += cost(id);
+            best[k].push_back(id);
+            total += cost(id);
+            cmax = std::max(cmax, cost(id));
         }
+        // first fit decreasing under the smallest capacity it packs, when
+        // that beats the longest-first makespan (items come in a few sizes,
+        // so the least-loaded rule often stacks two long items on a slot
+        // that a packing avoids)
+        auto ffd = [&](long cap, std::vector<std::vector<int>>* out) {
+            std::vector<long> ld(per_xcd, 0);
+            if (out) out->assign(per_xcd, {});
+            for (int id : wl) {
+                int k = 0;
+                while (k < per_xcd && ld[k] + cost(id) > cap) k++;
+                if (k == per_xcd) return false;
+                ld[k] += cost(id);
+                if (out) (*out)[k].push_back(id);
+            }
+            return true;
+        };
+        long lo = std::max(cmax, (total + per_xcd - 1) / per_xcd);
+        long hi = *std::max_element(sload.begin(), sload.end());  // ffd(hi) need not hold
+        if (lo < hi && ffd(hi - 1, nullptr)) {
+            hi = hi - 1;
+            while (lo < hi) {
+                const long mid = (lo + hi) / 2;
+                if (ffd(mid, nullptr)) hi = mid;
+                else lo = mid + 1;
+            }
+            ffd(hi, &best);
+        }
+        for (int k = 0; k < per_xcd; k++)
+            for (int id : best[k]) slot_work[x + XCDS * k].push_back(id);
     }
     P.sched_start.assign(n_slots + 1, 0);
     P.sched_desc.clear();

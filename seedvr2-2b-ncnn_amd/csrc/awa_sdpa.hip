@@ -79,9 +79,10 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 // keep LDS (128 B/clk/CU) as busy as the matrix cores.  K and V^T tiles reach
 // LDS by DMA (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
 // M0 + 16 i), K in a ring of three tile slots and V^T in a ring of two (80 KiB
-// per workgroup).  While an item works on its last tile, the next item's
-// first two K tiles and first V^T tile go into the free slots and, after its
-// last unit, the next query tile is loaded, so an item starts without memory
+// per workgroup).  The tiles a slot fetches form one stream across its
+// items: each tile fetches the K tile two ahead and the V^T tile one ahead,
+// so an item's last two tiles fetch the next item's first tiles, and after
+// its last unit the next query tile is loaded: an item starts without memory
 // round trips.
 //
 // The window's keys are processed in 32-key units u (two per tile).  With a
@@ -147,6 +148,37 @@ __device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
         :
         : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b] "s"(b), [m] "s"(m)
         : "memory", "m0");
+}
+// Single DMA instructions, for spreading a tile's DMA over the MFMA stream
+// one instruction at a time: byte offset 1024 o of base b (K) or of buffer r
+// (V), into LDS address m + 1024 o.
+__device__ __attribute__((always_inline)) inline void dma1_k(int o, uint64_t b, uint32_t vo, uint32_t m) {
+#define DMA1K(O)                                                                                   \
+    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v], %[b] offset:" #O \
+                 :                                                                                 \
+                 : [v] "v"(vo), [b] "s"(b), [m] "s"(m)                                             \
+                 : "memory", "m0")
+    switch (o) {
+        case 0: DMA1K(0); break;
+        case 1: DMA1K(1024); break;
+        case 2: DMA1K(2048); break;
+        default: DMA1K(3072); break;
+    }
+#undef DMA1K
+}
+__device__ __attribute__((always_inline)) inline void dma1_v(int o, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t m) {
+#define DMA1V(O)                                                                                          \
+    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v], %[r], 0 offen offset:" #O " lds" \
+                 :                                                                                        \
+                 : [v] "v"(vo), [r] "s"(r), [m] "s"(m)                                                    \
+                 : "memory", "m0")
+    switch (o) {
+        case 0: DMA1V(0); break;
+        case 1: DMA1V(1024); break;
+        case 2: DMA1V(2048); break;
+        default: DMA1V(3072); break;
+    }
+#undef DMA1V
 }
 // The eight instructions of a wave's K half tile: b1 = b0 + 16 rows.
 __device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4], uint32_t m) {
@@ -361,19 +393,36 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     auto tile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
         return kk < W.nvt ? W.vbase + kk : W.tbase + (kk - W.nvt);
     };
-    auto dma_k = [&](const Work& W, int kk, int slot) __attribute__((always_inline)) {
-        const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) +
-                                                        W.h * head_stride + (size_t)tile_of(W, kk) * KT_E);
-        dma_k8(src, src + 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot * KT_E + wave * (KT_E / 2)));
+    // The DMA stream of a slot is the key tiles of its items in order: tile kk
+    // of an item fetches K tile kk + 2 and V^T tile kk + 1 of the stream, which
+    // past the item's end are the next item's first tiles (an item has at
+    // least two key tiles, one of them text).  Past the slot's last item a
+    // tile fetches its own tile again into the free slot, so that every tile
+    // issues the same instructions (the kernel waits for these before it
+    // ends).  A tile's fetch: K source dk_src into LDS byte address dk_m, V^T
+    // rows (offsets vo) of buffer dv_r into dv_m.
+    uint64_t dk_src = 0;
+    uint32_t dk_m = 0, dv_m = 0;
+    __amdgpu_buffer_rsrc_t dv_r;
+    auto set_k = [&](int h, int tile, int slot) __attribute__((always_inline)) {
+        dk_src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) + h * head_stride +
+                                            (size_t)tile * KT_E);
+        dk_m = lds_base + 2 * (slot * KT_E + wave * (KT_E / 2));
+    };
+    // V^T of head h from the video or the text rows (the buffer starts 3 KiB
+    // early, so that the lane offsets of prep_v stay positive)
+    auto set_v = [&](int h, bool txt, int slot) __attribute__((always_inline)) {
+        const uint32_t col = 2 * (2 * DIM + h * HEAD_D) - 3072;
+        dv_r = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(txt ? a.tsrc : a.vsrc)) + col,
+                                                 0, (txt ? a.tsrc_bytes : a.vsrc_bytes) - col, 0x00020000);
+        dv_m = lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2));
     };
     // Row offsets of the next V tile to fetch (vt0: instructions 0-3, vt1:
     // 4-7), loaded one tile ahead with ordinary loads, so that the compiler
-    // waits for them before any use; vt_ok says whether they are there.
-    // prep_v turns them into this tile's DMA offsets at the start of a tile,
-    // before the tile issues any DMA of its own, so that this wait never
-    // waits for those.
+    // waits for them before any use.  prep_v turns them into this tile's DMA
+    // offsets at the start of a tile, before the tile issues any DMA of its
+    // own, so that this wait never waits for those.
     u32x4 vt0, vt1;
-    bool vt_ok = false;
     uint32_t vo[8];
     auto vtile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
         return kk < W.nvt ? W.vbase + kk : a.n_vid_tiles + (kk - W.nvt);
@@ -383,9 +432,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         vt0 = p[0];
         vt1 = p[1];
     };
-    auto prep_v = [&](const Work& W, int kk) __attribute__((always_inline)) {
-        if (!vt_ok) load_vt(vtile_of(W, kk));
-        vt_ok = true;
+    auto prep_v = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             vo[j] = vt0[j] * (2u * QKV) + vlane + (3072u - 1024u * j);
@@ -395,49 +442,19 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                           "+v"(vo[6]), "+v"(vo[7]));
     };
     auto wait_vmem = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-    // After the V DMA of key tile kk of W: the row offsets of the next V tile
-    // this slot fetches (tile kk + 1 of W, or tile 0 of the next item Y; when
-    // neither is known, tile kk again, marked as not there).  One load site,
-    // so that the registers need no copies, which would wait for the load.
-    auto after_v = [&](const Work& W, int kk, bool has_y, const Work& Y) __attribute__((always_inline)) {
-        const bool in_w = kk + 1 < W.nvt + a.ntt;
-        vt_ok = in_w || has_y;
-        load_vt(in_w ? vtile_of(W, kk + 1) : has_y ? vtile_of(Y, 0) : vtile_of(W, kk));
+    // instruction i (0-7) of the K and of the V^T fetch
+    auto dma_k_i = [&](int i) __attribute__((always_inline)) {
+        dma1_k(i & 3, i < 4 ? dk_src : dk_src + 2 * 16 * HEAD_D, koff[i & 3], i < 4 ? dk_m : dk_m + 4096);
     };
-    // Half h (instructions 4 h .. 4 h + 3) of the V DMA of key tile kk of W
-    // into ring slot `slot` (offsets from prep_v).
-    auto dma_v_half = [&](const Work& W, int kk, int slot, int h) __attribute__((always_inline)) {
-        const bool txt = kk >= W.nvt;
-        const uint32_t col = 2 * (2 * DIM + W.h * HEAD_D) - 3072;  // the buffer starts 3 KiB early
-        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<char*>(static_cast<const char*>(txt ? a.tsrc : a.vsrc)) + col, 0,
-            (txt ? a.tsrc_bytes : a.vsrc_bytes) - col, 0x00020000);
-        dma4_vrow(r, vo[4 * h], vo[4 * h + 1], vo[4 * h + 2], vo[4 * h + 3],
-                  lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2)) + 4096 * h);
+    auto dma_v_i = [&](int i) __attribute__((always_inline)) {
+        dma1_v(i & 3, dv_r, vo[i], i < 4 ? dv_m : dv_m + 4096);
     };
-    // The whole V DMA of key tile kk of W, then the next offsets.
-    auto dma_v = [&](const Work& W, int kk, int slot, bool has_y, const Work& Y) __attribute__((always_inline)) {
-        dma_v_half(W, kk, slot, 0);
-        dma_v_half(W, kk, slot, 1);
-        after_v(W, kk, has_y, Y);
+    auto dma_k_all = [&]() __attribute__((always_inline)) {
+        dma_k8(dk_src, dk_src + 2 * 16 * HEAD_D, koff, dk_m);
     };
-    // Quarter q of the DMA of key tile kk (K half q for q < 2, V half q - 2).
-    auto dma_quarter = [&](const Work& W, int q, int kk_k, int slot_k, int kk_v, int slot_v, bool has_y,
-                           const Work& Y) __attribute__((always_inline)) {
-        if (q < 2) {
-            const uint64_t src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) +
-                                                            W.h * head_stride + (size_t)tile_of(W, kk_k) * KT_E);
-            dma4_k(src + q * 2 * 16 * HEAD_D, koff, lds_base + 2 * (slot_k * KT_E + wave * (KT_E / 2)) + 4096 * q);
-        } else {
-            dma_v_half(W, kk_v, slot_v, q - 2);
-            if (q == 3) after_v(W, kk_v, has_y, Y);
-        }
-    };
-    // The first K tiles and V tile of W into ring slots kb, kb + 1 and vb.
-    auto dma_first = [&](const Work& W, int kb, int vb, bool has_y, const Work& Y) __attribute__((always_inline)) {
-        dma_k(W, 0, kb);
-        if (W.nvt + a.ntt > 1) dma_k(W, 1, (kb + 1) % 3);
-        dma_v(W, 0, vb, has_y, Y);
+    auto dma_v_all = [&]() __attribute__((always_inline)) {
+        dma4_vrow(dv_r, vo[0], vo[1], vo[2], vo[3], dv_m);
+        dma4_vrow(dv_r, vo[4], vo[5], vo[6], vo[7], dv_m + 4096);
     };
     // B operand of S^T = K Q^T for column block qb, k-step s:
     // Q[slot 32 qb + n][16 s + 8 hb .. +8]
@@ -484,8 +501,17 @@ void sdpa_bf16_kernel(SdpaArgs a) {
 
     Work cur = load_work(desc, wi0);
     int kb = 0, vb = 0;  // ring slots of the current item's key tile 0
-    prep_v(cur, 0);
-    dma_first(cur, kb, vb, false, cur);
+    // the stream's first K tiles and V^T tile, then the row offsets of the
+    // V^T tile that tile 0 fetches
+    load_vt(vtile_of(cur, 0));
+    prep_v();
+    set_k(cur.h, tile_of(cur, 0), 0);
+    dma_k_all();
+    set_k(cur.h, tile_of(cur, 1), 1);
+    dma_k_all();
+    set_v(cur.h, 0 >= cur.nvt, 0);
+    dma_v_all();
+    load_vt(vtile_of(cur, 1));
     load_q(cur);
 
     for (int wi = wi0; wi < wi1; wi++) {
@@ -554,12 +580,14 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             }
         }
 
+        int nv_tile = 0;  // V^T tile whose row offsets the current tile loads
         // One unit: phases A and B as described above.
-        // dk / dv: the unit also issues the tile's DMA of K tile kk_k into slot
-        // sk / V^T tile kk_v into slot sv, a quarter after each fourth score
-        // slot (the MFMAs run while the DMA instructions issue).
-        auto unit = [&](int u, bool has_succ, bool dk, bool dv, int kk_k, int sk, int kk_v, int sv)
-            __attribute__((always_inline)) {
+        // dma: the unit also issues its tile's fetch, one DMA instruction per
+        // score MFMA from the third on (K, then V^T, then the next row
+        // offsets): a 1 KiB instruction occupies the CU's address unit for 16
+        // cycles, so issued back to back they would stall the wave, while one
+        // per 32-cycle MFMA goes through without a stall.
+        auto unit = [&](int u, bool has_succ, bool dma) __attribute__((always_inline)) {
             // ---- stale-maximum rule for this unit's scores (mtc: their row max relative to m)
             if (__any(mtc[0] > RESCALE_LOG2 || mtc[1] > RESCALE_LOG2)) {
                 float alpha[2];
@@ -630,9 +658,13 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     if (j < 16) __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     if (j == 3) load_vf();
-                    if ((j == 4 || j == 8) && dk) dma_quarter(cur, j / 8, kk_k, sk, kk_v, sv, has_next, nxt);
-                    if ((j == 12 || j == 16) && dv)
-                        dma_quarter(cur, 2 + (j - 12) / 4, kk_k, sk, kk_v, sv, has_next, nxt);
+                    if (dma && j >= 2 && j < 10) dma_k_i(j - 2);
+                    if (dma && j >= 10) dma_v_i(j - 10);
+                    if (dma && j == 17) load_vt(nv_tile);
+                    // the DMA asm belongs to no scheduling group, so the
+                    // scheduler would gather the sixteen instructions into a
+                    // burst; a full scheduling barrier keeps each at its slot
+                    if (dma && j >= 2) __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
                 load_vf();
@@ -681,23 +713,42 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         // the current and next score registers alternate without copies); the
         // last tile is peeled because its second unit has no successor.
         auto tile = [&](int kk, bool last) __attribute__((always_inline)) {
-            const bool dk = kk + 2 < nk, dv = kk + 1 < nk;
-            const int sk = (kb + kk + 2) % 3, sv = (vb + kk + 1) & 1;
-            // this tile's V DMA: tile kk + 1, or the next item's first tile
-            if (dv) prep_v(cur, kk + 1);
-            else if (last && has_next) prep_v(nxt, 0);
-            if (last && has_next) dma_first(nxt, (kb + nk) % 3, (vb + nk) & 1, false, nxt);
+            // this tile's fetch (K tile kk + 2 and V^T tile kk + 1 of the
+            // stream) and the V^T tile of the next tile's fetch
+            // (values, not a choice between the two items' fields: a
+            // conditional lvalue keeps both items in scratch memory)
+            int kh = cur.h, kt = tile_of(cur, kk), vh = cur.h;
+            bool vtxt = kk >= cur.nvt;
+            nv_tile = vtile_of(cur, min(kk + 1, nk - 1));
+            if (kk + 2 < nk) {
+                kt = tile_of(cur, kk + 2);
+                nv_tile = vtile_of(cur, kk + 2);
+            } else if (has_next) {
+                kh = nxt.h;
+                kt = tile_of(nxt, kk + 2 - nk);
+                nv_tile = vtile_of(nxt, kk + 2 - nk);
+            }
+            if (kk + 1 < nk) {
+                vtxt = kk + 1 >= cur.nvt;
+            } else if (has_next) {
+                vh = nxt.h;
+                vtxt = 0 >= nxt.nvt;
+            }
+            set_k(kh, kt, (kb + kk + 2) % 3);
+            set_v(vh, vtxt, (vb + kk + 1) & 1);
+            prep_v();
             if (active) {
-                unit(2 * kk, true, dk, dv, kk + 2, sk, kk + 1, sv);
+                unit(2 * kk, true, true);
             } else {  // an idle wave still fills its half of the tiles
-                if (dk) dma_k(cur, kk + 2, sk);
-                if (dv) dma_v(cur, kk + 1, sv, has_next, nxt);
+                dma_k_all();
+                dma_v_all();
+                load_vt(nv_tile);
             }
             // the item's last unit computes no scores: Q is dead, so the
             // next item's query tile loads during it (after the slot's last
             // item: the same tile again, unused)
             if (last) load_q(nxt);
-            if (active) unit(2 * kk + 1, !last, false, false, 0, 0, 0, 0);
+            if (active) unit(2 * kk + 1, !last, false);
             if (!last) {
                 wait_vmem();
                 __syncthreads();
@@ -776,6 +827,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         vb = (vb + nk) & 1;
         cur = nxt;
     }
+    wait_vmem();  // the last tiles' fetches and query loads land before the workgroup's LDS is released
 }
 
 }  // namespace
