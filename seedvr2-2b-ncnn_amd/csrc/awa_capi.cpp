@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <map>
 #include <vector>
 
 #include "awa_internal.hpp"
@@ -94,6 +95,10 @@ void free_geom_buffers(awa_geom* g) {
         if (p) (void)hipFree(p);
 }
 
+}  // namespace
+
+namespace awa {
+
 // 64-row tiles of every window plus the text tiles, and the work items of the
 // attention kernel (one window, two query tiles).
 void plan_tiles(GeomPlan& P) {
@@ -134,7 +139,7 @@ void plan_tiles(GeomPlan& P) {
     P.n_items = (int)P.items.size() / 4;
 }
 
-// Static longest-processing-time schedule of the persistent bf16 attention
+// Static schedule of the persistent bf16 attention
 // kernel over n_slots resident workgroups.  A work item costs about its
 // window's key-tile count plus two and a half tiles of per-item work (first
 // scores, the wait for the query tile, the epilogue), as timed per wave on
@@ -207,6 +212,31 @@ void plan_schedule(GeomPlan& P, int n_slots) {
                 else lo = mid + 1;
             }
             ffd(hi, &best);
+            // The packing fixes each slot's sequence of item sizes; hand out
+            // the items position by position over the slots (slots with equal
+            // sequences adjacent), so that the items of one (window, head),
+            // which have equal sizes and lie together in wl, run at the same
+            // time on neighbouring slots and share the window's tiles in L2
+            // rather than fetching them again at different times.
+            std::vector<std::vector<long>> pat(per_xcd);
+            size_t plen = 0;
+            for (int k = 0; k < per_xcd; k++) {
+                for (int id : best[k]) pat[k].push_back(cost(id));
+                plen = std::max(plen, pat[k].size());
+            }
+            std::vector<int> order(per_xcd);
+            for (int k = 0; k < per_xcd; k++) order[k] = k;
+            std::stable_sort(order.begin(), order.end(), [&](int u, int v) { return pat[u] > pat[v]; });
+            std::map<long, std::vector<int>> queue;  // size -> ids in wl order
+            for (int id : wl) queue[cost(id)].push_back(id);
+            std::map<long, size_t> next;
+            for (int k = 0; k < per_xcd; k++) best[k].clear();
+            for (size_t pos = 0; pos < plen; pos++)
+                for (int k : order)
+                    if (pos < pat[k].size()) {
+                        const long c = pat[k][pos];
+                        best[k].push_back(queue[c][next[c]++]);
+                    }
         }
         for (int k = 0; k < per_xcd; k++)
             for (int id : best[k]) slot_work[x + XCDS * k].push_back(id);
@@ -227,6 +257,10 @@ void plan_schedule(GeomPlan& P, int n_slots) {
         P.sched_start[sl + 1] = n;
     }
 }
+
+}  // namespace awa
+
+namespace {
 
 int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
     GeomPlan& P = g->plan;

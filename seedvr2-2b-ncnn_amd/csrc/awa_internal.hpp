@@ -111,6 +111,11 @@ struct GeomPlan {
     std::vector<int32_t> sched_start;  // n_slots+1
     std::vector<int32_t> sched_desc;   // 8 per item, n_items*HEADS items
 };
+// Host planning (awa_capi.cpp): the tiles and work items of a geometry with
+// nwin, cumf, txt_len and txt_sets set, then the attention kernel's
+// schedule over n_slots workgroups (a multiple of 8 is used).
+void plan_tiles(GeomPlan& P);
+void plan_schedule(GeomPlan& P, int n_slots);
 // Row table (awa_geom::d_vrow): per row tile (the video tiles, then ntt
 // text tiles shared by all windows) the 64 row indices of its rows in vqkv
 // (video, through vidx) or tqkv (text); rows past the end of a window or of

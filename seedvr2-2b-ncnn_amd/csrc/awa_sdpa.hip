@@ -77,7 +77,7 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 // tile as two 32-query column blocks (qb), so each K or V^T fragment read from
 // LDS feeds two MFMAs: with 32 queries per wave the fragment reads alone would
 // keep LDS (128 B/clk/CU) as busy as the matrix cores.  K and V^T tiles reach
-// LDS by DMA (global_load_lds_dwordx4: lane i of a wave writes 16 bytes at
+// LDS by DMA (buffer_load_dwordx4 ... lds: lane i of a wave writes 16 bytes at
 // M0 + 16 i), K in a ring of three tile slots and V^T in a ring of two (80 KiB
 // per workgroup).  The tiles a slot fetches form one stream across its
 // items: each tile fetches the K tile two ahead and the V^T tile one ahead,
@@ -135,28 +135,31 @@ typedef __attribute__((address_space(3))) bf16x4 lbf16x4_t;
 // loads itself (vmcnt(0) and a barrier) before any wave reads the tiles they
 // fill.  M0 written by an SALU instruction needs one wait state before the
 // DMA reads it.
-// K: four instructions from global base b with lane offsets vo[0..3].
+// K: four instructions from buffer r (one tile) at SGPR offset so with lane
+// offsets vo[0..3].
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ inline void dma4_k(uint64_t b, const uint32_t (&vo)[4], uint32_t m) {
+__device__ inline void dma4_k(__amdgpu_buffer_rsrc_t r, uint32_t so, const uint32_t (&vo)[4], uint32_t m) {
     asm volatile(
         "s_mov_b32 m0, %[m]\n\ts_nop 0\n\t"
-        "global_load_lds_dwordx4 %[v0], %[b]\n\t"
-        "global_load_lds_dwordx4 %[v1], %[b] offset:1024\n\t"
-        "global_load_lds_dwordx4 %[v2], %[b] offset:2048\n\t"
-        "global_load_lds_dwordx4 %[v3], %[b] offset:3072"
+        "buffer_load_dwordx4 %[v0], %[r], %[so] offen lds\n\t"
+        "buffer_load_dwordx4 %[v1], %[r], %[so] offen offset:1024 lds\n\t"
+        "buffer_load_dwordx4 %[v2], %[r], %[so] offen offset:2048 lds\n\t"
+        "buffer_load_dwordx4 %[v3], %[r], %[so] offen offset:3072 lds"
         :
-        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [b] "s"(b), [m] "s"(m)
+        : [v0] "v"(vo[0]), [v1] "v"(vo[1]), [v2] "v"(vo[2]), [v3] "v"(vo[3]), [r] "s"(r), [so] "s"(so),
+          [m] "s"(m)
         : "memory", "m0");
 }
 // Single DMA instructions, for spreading a tile's DMA over the MFMA stream
-// one instruction at a time: byte offset 1024 o of base b (K) or of buffer r
-// (V), into LDS address m + 1024 o.
-__device__ __attribute__((always_inline)) inline void dma1_k(int o, uint64_t b, uint32_t vo, uint32_t m) {
-#define DMA1K(O)                                                                                   \
-    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v], %[b] offset:" #O \
-                 :                                                                                 \
-                 : [v] "v"(vo), [b] "s"(b), [m] "s"(m)                                             \
+// one instruction at a time: byte offset 1024 o of buffer r (plus SGPR offset
+// so for K), into LDS address m + 1024 o.
+__device__ __attribute__((always_inline)) inline void dma1_k(int o, __amdgpu_buffer_rsrc_t r, uint32_t so, uint32_t vo,
+                                                             uint32_t m) {
+#define DMA1K(O)                                                                                                   \
+    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v], %[r], %[so] offen offset:" #O " lds" \
+                 :                                                                                                 \
+                 : [v] "v"(vo), [r] "s"(r), [so] "s"(so), [m] "s"(m)                                              \
                  : "memory", "m0")
     switch (o) {
         case 0: DMA1K(0); break;
@@ -180,10 +183,10 @@ __device__ __attribute__((always_inline)) inline void dma1_v(int o, __amdgpu_buf
     }
 #undef DMA1V
 }
-// The eight instructions of a wave's K half tile: b1 = b0 + 16 rows.
-__device__ inline void dma_k8(uint64_t b0, uint64_t b1, const uint32_t (&vo)[4], uint32_t m) {
-    dma4_k(b0, vo, m);
-    dma4_k(b1, vo, m + 4096);
+// The eight instructions of a wave's K half tile (the second four 16 rows on).
+__device__ inline void dma_k8(__amdgpu_buffer_rsrc_t r, const uint32_t (&vo)[4], uint32_t m) {
+    dma4_k(r, 0, vo, m);
+    dma4_k(r, 4096, vo, m + 4096);
 }
 // V rows: four instructions from buffer r (a head's V columns of vqkv or
 // tqkv, based 3 KiB early so that the compensated offsets stay positive; an
@@ -399,22 +402,23 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // least two key tiles, one of them text).  Past the slot's last item a
     // tile fetches its own tile again into the free slot, so that every tile
     // issues the same instructions (the kernel waits for these before it
-    // ends).  A tile's fetch: K source dk_src into LDS byte address dk_m, V^T
-    // rows (offsets vo) of buffer dv_r into dv_m.
-    uint64_t dk_src = 0;
+    // ends; those fetches get empty buffers, whose loads write zeros without
+    // touching memory).  A tile's fetch: K tile buffer dk_r into LDS byte
+    // address dk_m, V^T rows (offsets vo) of buffer dv_r into dv_m.
+    __amdgpu_buffer_rsrc_t dk_r, dv_r;
     uint32_t dk_m = 0, dv_m = 0;
-    __amdgpu_buffer_rsrc_t dv_r;
-    auto set_k = [&](int h, int tile, int slot) __attribute__((always_inline)) {
-        dk_src = reinterpret_cast<uint64_t>(reinterpret_cast<const uint16_t*>(a.Kp) + h * head_stride +
-                                            (size_t)tile * KT_E);
+    auto set_k = [&](int h, int tile, int slot, bool real) __attribute__((always_inline)) {
+        dk_r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(a.Kp) + h * head_stride + (size_t)tile * KT_E), 0,
+            real ? 2 * KT_E : 0, 0x00020000);
         dk_m = lds_base + 2 * (slot * KT_E + wave * (KT_E / 2));
     };
     // V^T of head h from the video or the text rows (the buffer starts 3 KiB
     // early, so that the lane offsets of prep_v stay positive)
-    auto set_v = [&](int h, bool txt, int slot) __attribute__((always_inline)) {
+    auto set_v = [&](int h, bool txt, int slot, bool real) __attribute__((always_inline)) {
         const uint32_t col = 2 * (2 * DIM + h * HEAD_D) - 3072;
         dv_r = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(txt ? a.tsrc : a.vsrc)) + col,
-                                                 0, (txt ? a.tsrc_bytes : a.vsrc_bytes) - col, 0x00020000);
+                                                 0, real ? (txt ? a.tsrc_bytes : a.vsrc_bytes) - col : 0, 0x00020000);
         dv_m = lds_base + 2 * ((3 + slot) * KT_E + wave * (KT_E / 2));
     };
     // Row offsets of the next V tile to fetch (vt0: instructions 0-3, vt1:
@@ -444,13 +448,13 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     auto wait_vmem = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
     // instruction i (0-7) of the K and of the V^T fetch
     auto dma_k_i = [&](int i) __attribute__((always_inline)) {
-        dma1_k(i & 3, i < 4 ? dk_src : dk_src + 2 * 16 * HEAD_D, koff[i & 3], i < 4 ? dk_m : dk_m + 4096);
+        dma1_k(i & 3, dk_r, i < 4 ? 0u : 4096u, koff[i & 3], i < 4 ? dk_m : dk_m + 4096);
     };
     auto dma_v_i = [&](int i) __attribute__((always_inline)) {
         dma1_v(i & 3, dv_r, vo[i], i < 4 ? dv_m : dv_m + 4096);
     };
     auto dma_k_all = [&]() __attribute__((always_inline)) {
-        dma_k8(dk_src, dk_src + 2 * 16 * HEAD_D, koff, dk_m);
+        dma_k8(dk_r, koff, dk_m);
     };
     auto dma_v_all = [&]() __attribute__((always_inline)) {
         dma4_vrow(dv_r, vo[0], vo[1], vo[2], vo[3], dv_m);
@@ -505,11 +509,11 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     // V^T tile that tile 0 fetches
     load_vt(vtile_of(cur, 0));
     prep_v();
-    set_k(cur.h, tile_of(cur, 0), 0);
+    set_k(cur.h, tile_of(cur, 0), 0, true);
     dma_k_all();
-    set_k(cur.h, tile_of(cur, 1), 1);
+    set_k(cur.h, tile_of(cur, 1), 1, true);
     dma_k_all();
-    set_v(cur.h, 0 >= cur.nvt, 0);
+    set_v(cur.h, 0 >= cur.nvt, 0, true);
     dma_v_all();
     load_vt(vtile_of(cur, 1));
     load_q(cur);
@@ -734,8 +738,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 vh = nxt.h;
                 vtxt = 0 >= nxt.nvt;
             }
-            set_k(kh, kt, (kb + kk + 2) % 3);
-            set_v(vh, vtxt, (vb + kk + 1) & 1);
+            set_k(kh, kt, (kb + kk + 2) % 3, kk + 2 < nk || has_next);
+            set_v(vh, vtxt, (vb + kk + 1) & 1, kk + 1 < nk || has_next);
             prep_v();
             if (active) {
                 unit(2 * kk, true, true);
