@@ -289,6 +289,10 @@ int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
     HIPCK(ctx, hipMemcpyAsync(g->d_tile_meta, P.tile_meta.data(), P.tile_meta.size() * 4,
                               hipMemcpyHostToDevice, s));
     // the row table (needs d_cumf and d_vidx)
+    if (P.Lv > VROW_MAX_OFFSET_ROWS || P.txt_len > VROW_MAX_OFFSET_ROWS) {
+        set_err(ctx, "geometry: %d video / %d text rows exceed the row table's 32-bit offsets", P.Lv, P.txt_len);
+        return AWA_EARG;
+    }
     HIPCK(ctx, dalloc(&g->d_vrow, (size_t)(P.n_vid_tiles + P.ntt) * TILE));
     HIPCK(ctx, launch_vrow(g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win, P.n_vid_tiles, P.ntt,
                            P.txt_len, g->d_vrow, s));

@@ -146,8 +146,8 @@ __global__ __launch_bounds__(256) void geom_tables_kernel(const float* __restric
 }
 
 // The row table (layout and clamping in awa_internal.hpp): entry
-// [tile][w][g][j] holds the index of row 32 w + 4 j + g of the tile in vqkv
-// (video tiles, through vidx) or tqkv.
+// [tile][w][g][j] holds the element offset (index x 7680) of row 32 w + 4 j + g
+// of the tile in vqkv (video tiles, through vidx) or tqkv.
 __global__ __launch_bounds__(256) void vrow_kernel(const int32_t* __restrict__ cumf,
                                                    const int32_t* __restrict__ vidx,
                                                    const int32_t* __restrict__ tile_base,
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void vrow_kernel(const int32_t* __restrict__ c
         } else {
             row = min((tile - n_vid_tiles) * TILE + R, txt_len - 1);
         }
-        vrow[e] = (uint32_t)row;
+        vrow[e] = (uint32_t)row * (uint32_t)QKV;
     }
 }
 

@@ -117,13 +117,15 @@ struct GeomPlan {
 void plan_tiles(GeomPlan& P);
 void plan_schedule(GeomPlan& P, int n_slots);
 // Row table (awa_geom::d_vrow): per row tile (the video tiles, then ntt
-// text tiles shared by all windows) the 64 row indices of its rows in vqkv
-// (video, through vidx) or tqkv (text); rows past the end of a window or of
-// the text repeat its last row.  Stored so that the lane of the bf16
+// text tiles shared by all windows) the element offsets (row index x 7680) of
+// its 64 rows in vqkv (video, through vidx) or tqkv (text); rows past the end
+// of a window or of the text repeat its last row.  Stored so that the lane of the bf16
 // attention kernel that fetches row 32 w + 4 j + g of a tile (w: wave,
 // g = lane / 16) finds its eight rows at [tile][w][g][j]; vrow_pos gives the
-// position of row r.  The attention kernel's byte offsets (row * 7680 * 2)
-// are 32-bit, which bounds the rows of the bf16 path.
+// position of row r.  The offsets are 32-bit (VROW_MAX_OFFSET_ROWS rows),
+// and so are the bf16 attention kernel's byte offsets (twice them), which
+// bounds the rows of the bf16 path (VROW_MAX_ROWS).
+constexpr long VROW_MAX_OFFSET_ROWS = 0xffffffffL / QKV;
 constexpr long VROW_MAX_ROWS = 0xffffffffL / (2L * QKV);
 __host__ __device__ inline int vrow_pos(int r) { return 32 * (r >> 5) + 8 * (r & 3) + ((r & 31) >> 2); }
 

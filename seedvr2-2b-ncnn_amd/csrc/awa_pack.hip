@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
         if (r < nvalid) {  // uniform across the 16 lanes of a row
-            const T* row = src + (size_t)ridx[kk] * QKV + col;
+            const T* row = src + (size_t)ridx[kk] + col;
             rq[kk] = IO::load(row);
             rk[kk] = IO::load(row + DIM);
             if constexpr (kV) rv[kk] = IO::load(row + 2 * DIM);

@@ -439,8 +439,8 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     auto prep_v = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            vo[j] = vt0[j] * (2u * QKV) + vlane + (3072u - 1024u * j);
-            vo[4 + j] = vt1[j] * (2u * QKV) + vlane + (3072u - 1024u * j);
+            vo[j] = (vt0[j] << 1) + vlane + (3072u - 1024u * j);
+            vo[4 + j] = (vt1[j] << 1) + vlane + (3072u - 1024u * j);
         }
         asm volatile("" : "+v"(vo[0]), "+v"(vo[1]), "+v"(vo[2]), "+v"(vo[3]), "+v"(vo[4]), "+v"(vo[5]),
                           "+v"(vo[6]), "+v"(vo[7]));
