@@ -153,14 +153,19 @@ __device__ inline void dma4_k(__amdgpu_buffer_rsrc_t r, uint32_t so, const uint3
 }
 // Single DMA instructions, for spreading a tile's DMA over the MFMA stream
 // one instruction at a time: byte offset 1024 o of buffer r (plus SGPR offset
-// so for K), into LDS address m + 1024 o.
-__device__ __attribute__((always_inline)) inline void dma1_k(int o, __amdgpu_buffer_rsrc_t r, uint32_t so, uint32_t vo,
-                                                             uint32_t m) {
-#define DMA1K(O)                                                                                                   \
-    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v], %[r], %[so] offen offset:" #O " lds" \
-                 :                                                                                                 \
-                 : [v] "v"(vo), [r] "s"(r), [so] "s"(so), [m] "s"(m)                                              \
-                 : "memory", "m0")
+// so for K), into LDS address M0 + 1024 o.  M0 is set by m0_set, once per
+// four instructions, and nothing else in the kernel writes M0 (the compiler
+// has no use for it in this code: a test checks its assembly for that); the
+// asm statements are volatile, so they keep their order.
+__device__ __attribute__((always_inline)) inline void m0_set(uint32_t m) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0" : : "s"(m) : "m0");
+}
+__device__ __attribute__((always_inline)) inline void dma1_k(int o, __amdgpu_buffer_rsrc_t r, uint32_t so, uint32_t vo) {
+#define DMA1K(O)                                                                          \
+    asm volatile("buffer_load_dwordx4 %[v], %[r], %[so] offen offset:" #O " lds"          \
+                 :                                                                        \
+                 : [v] "v"(vo), [r] "s"(r), [so] "s"(so)                                  \
+                 : "memory")
     switch (o) {
         case 0: DMA1K(0); break;
         case 1: DMA1K(1024); break;
@@ -169,12 +174,12 @@ __device__ __attribute__((always_inline)) inline void dma1_k(int o, __amdgpu_buf
     }
 #undef DMA1K
 }
-__device__ __attribute__((always_inline)) inline void dma1_v(int o, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t m) {
-#define DMA1V(O)                                                                                          \
-    asm volatile("s_mov_b32 m0, %[m]\n\ts_nop 0\n\tbuffer_load_dwordx4 %[v], %[r], 0 offen offset:" #O " lds" \
-                 :                                                                                        \
-                 : [v] "v"(vo), [r] "s"(r), [m] "s"(m)                                                    \
-                 : "memory", "m0")
+__device__ __attribute__((always_inline)) inline void dma1_v(int o, __amdgpu_buffer_rsrc_t r, uint32_t vo) {
+#define DMA1V(O)                                                                                  \
+    asm volatile("buffer_load_dwordx4 %[v], %[r], 0 offen offset:" #O " lds"                      \
+                 :                                                                                \
+                 : [v] "v"(vo), [r] "s"(r)                                                        \
+                 : "memory")
     switch (o) {
         case 0: DMA1V(0); break;
         case 1: DMA1V(1024); break;
@@ -447,11 +452,16 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     };
     auto wait_vmem = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
     // instruction i (0-7) of the K and of the V^T fetch
+    // instruction i (0-7) of the K fetch, then of the V^T fetch, with the M0
+    // write each fourth one needs issued after the one before
     auto dma_k_i = [&](int i) __attribute__((always_inline)) {
-        dma1_k(i & 3, dk_r, i < 4 ? 0u : 4096u, koff[i & 3], i < 4 ? dk_m : dk_m + 4096);
+        dma1_k(i & 3, dk_r, i < 4 ? 0u : 4096u, koff[i & 3]);
+        if (i == 3) m0_set(dk_m + 4096);
+        if (i == 7) m0_set(dv_m);
     };
     auto dma_v_i = [&](int i) __attribute__((always_inline)) {
-        dma1_v(i & 3, dv_r, vo[i], i < 4 ? dv_m : dv_m + 4096);
+        dma1_v(i & 3, dv_r, vo[i]);
+        if (i == 3) m0_set(dv_m + 4096);
     };
     auto dma_k_all = [&]() __attribute__((always_inline)) {
         dma_k8(dk_r, koff, dk_m);
@@ -641,6 +651,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 bf16x8 kf[8];
                 const int ko = k_ofs(u + 1);
                 const bf16x8 onesm = mask_frag(unit_kv(u + 1), n, hb);
+                if (dma) m0_set(dk_m);
 #pragma unroll
                 for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the eight K fragment reads first

@@ -10,7 +10,10 @@ under register pressure), the use would read stale data without any error.
 This test compiles the kernel to AMD assembly with the library's own flags
 (Makefile) and proves on its control-flow graph that on every path from such a
 load no instruction touches the loaded registers before an `s_waitcnt
-vmcnt(0)`.  The analysis is checked on planted mistakes first.
+vmcnt(0)`.  The analysis is checked on planted mistakes first.  A second
+check: the kernel's LDS DMA takes its destination from M0, written by the
+kernel's asm once per four DMA instructions, so no compiler-generated
+instruction may write M0 anywhere in the kernel.
 """
 import os
 import re
@@ -178,3 +181,42 @@ def test_query_fragment_loads_are_waited_for(sdpa_asm):
     violations, n_loads = check(parse(sdpa_asm))
     assert n_loads >= 16, "no asm query-fragment loads found: the check would be vacuous"
     assert not violations, violations[:5]
+
+
+M0_WRITE = re.compile(r"^\s*s_\w+\s+m0\b")
+
+
+def m0_writes(asm_text):
+    """Instructions of the kernel that write M0, split into those inside the
+    kernel's own inline asm (between ;;#ASMSTART and ;;#ASMEND) and the rest."""
+    lines = asm_text.split("\n")
+    start = next(i for i, l in enumerate(lines) if l.startswith(KERNEL + ":"))
+    inside, outside, in_asm = [], [], False
+    for l in lines[start + 1:]:
+        if l.startswith(".Lfunc_end"):
+            break
+        if ";;#ASMSTART" in l:
+            in_asm = True
+            continue
+        if ";;#ASMEND" in l:
+            in_asm = False
+            continue
+        s = l.split(";")[0]
+        if M0_WRITE.match(s):
+            (inside if in_asm else outside).append(s.strip())
+    return inside, outside
+
+
+def test_m0_written_only_by_the_kernels_asm(sdpa_asm):
+    """The kernel's LDS DMA instructions take their LDS address from M0, which
+    its own asm sets once per four instructions, the instructions issued one by
+    one between score MFMAs.  A compiler-generated M0 write anywhere in the
+    kernel could land between such a write and its instructions and send the
+    DMA elsewhere in LDS, so there must be none."""
+    inside, outside = m0_writes(sdpa_asm)
+    assert len(inside) >= 8, "no asm M0 writes found: the check would be vacuous"
+    assert not outside, outside[:5]
+    # a planted compiler-style write outside the asm is found
+    planted = sdpa_asm.replace(";;#ASMSTART", "\ts_mov_b32 m0, -1\n\t;;#ASMSTART", 1)
+    _, outside2 = m0_writes(planted)
+    assert outside2 == ["s_mov_b32 m0, -1"]
