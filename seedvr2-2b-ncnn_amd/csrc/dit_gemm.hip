@@ -11,8 +11,10 @@
 // on random bf16 data the part holds 1.86 GHz with it against 1.65 GHz with
 // 32x32x16 (measured), and a full GEMM here runs at the power limit.
 //
-// Workgroup tile 256 (n) x 256 (m), K step 64, four wave64 in a 2x2 grid of
-// 128x128 wave tiles (64 accumulators of 16x16 per wave).  Operand k-slices
+// Workgroup tile 256 (n) x 256 (m) or 256 x 224 (whichever fills the CUs in
+// fewer rounds per row of tile; launch_gemm), K step 64, four wave64 in a 2x2
+// grid of 128 x 128 (or 128 x 112) wave tiles, 64 (or 56) accumulators of
+// 16x16 per wave.  Operand k-slices
 // reach LDS by direct buffer->LDS DMA (buffer_load_dwordx4 ... lds) into two
 // 64 KiB stages: while one stage is computed the next one lands.  LDS rows
 // are 128 bytes (64 k of one operand row), so every DMA instruction reads
@@ -68,14 +70,14 @@ __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ (
 // Accumulator layout: acc[i][j] is the 16x16 block of output features
 // n_base + 16 i + .. and rows m_base + 16 j + ..; lane (col = lane % 16,
 // q = lane / 16) holds row 16 j + col, features 16 i + 4 q + t in register t.
-template <int EPI>
-__device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], int n_base,
+template <int EPI, int MJ>
+__device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ], int n_base,
                                 int m_base, int lane, uint16_t* stg) {
     const int q = lane >> 4, col = lane & 15;
     if constexpr (EPI == EPI_STORE) {
         // staged rows: 128 features bf16 = 256 bytes, 16 chunks of 8
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < MJ; j++) {
             const int r = 16 * j + col;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -89,7 +91,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
         const int c = lane & 15;
         uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + n_base + c * 8;
 #pragma unroll 8
-        for (int it = 0; it < 32; it++) {
+        for (int it = 0; it < 4 * MJ; it++) {
             const int r = 4 * it + (lane >> 4), m = m_base + r;
             const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 128 + ((c ^ (r & 15)) << 3));
             if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
@@ -99,7 +101,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
         // (in, gate) of output features 32 h + 16 e + ..; staged rows: 64
         // features bf16 = 128 bytes, 8 chunks of 8
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < MJ; j++) {
             const int r = 16 * j + col;
 #pragma unroll
             for (int h = 0; h < 2; h++)
@@ -125,7 +127,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
         const int c = lane & 7;
         uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + (n_base >> 1) + c * 8;
 #pragma unroll 8
-        for (int it = 0; it < 16; it++) {
+        for (int it = 0; it < 2 * MJ; it++) {
             const int r = 8 * it + (lane >> 3), m = m_base + r;
             const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3));
             if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
@@ -135,7 +137,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
 #pragma unroll
         for (int half = 0; half < 2; half++) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
+            for (int j = 0; j < MJ; j++) {
                 const int r = 16 * j + col;
 #pragma unroll
                 for (int i2 = 0; i2 < 4; i2++) {
@@ -154,7 +156,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
             const float4 g1 = p.gate1 ? *reinterpret_cast<const float4*>(p.gate1 + n) : one;
             float* out = reinterpret_cast<float*>(p.C) + n;
 #pragma unroll 8
-            for (int it = 0; it < 32; it++) {
+            for (int it = 0; it < 4 * MJ; it++) {
                 const int r = 4 * it + (lane >> 4), m = m_base + r;
                 const float4 v = *reinterpret_cast<const float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2));
                 if (m < p.M) {
@@ -173,8 +175,9 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][8], 
     }
 }
 
-template <int EPI>
+template <int EPI, int MJ>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
+    constexpr int BMT = 32 * MJ;  // rows of A per tile (LDS is laid out for BM)
     __shared__ __align__(16) uint16_t lds[NSTAGE * STAGE_E];
     const int lid = xcd_remap(b.total_tiles);
     if (lid >= b.total_tiles) return;
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     const int in_group = local % (GM * p.n_tiles);
     const int mt = first_m + in_group % gm;
     const int nt = in_group / gm;
-    const int n0 = nt * BN, m0 = mt * BM;
+    const int n0 = nt * BN, m0 = mt * BMT;
 
     // wave is uniform: read into a scalar so that the LDS-DMA destinations
     // (M0) are formed by scalar instructions, without v_readfirstlane
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     // measurably faster than global loads with 64-bit lane addresses.  Rows
     // of A past M repeat the last row; the resource range bounds every read.
     const uint16_t* Ap = p.A + (size_t)m0 * p.lda;
-    const int arows = min(BM, p.M - m0);
+    const int arows = min(BMT, p.M - m0);  // LDS rows past BMT are fetched (clamped) but unused
     int woff[8], aoff[8];   // byte offsets of this lane's 16 bytes at k = 0
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -232,22 +235,21 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
         for (int g = 0; g < 16; g++) load_piece(kt, slot, g);
     };
 
-    f32x4 acc[8][8];
+    f32x4 acc[8][MJ];
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < MJ; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int nk = p.K / BK;
-    int wrow[8], arow[8];
+    int wrow[8], arow[MJ];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        wrow[i] = wn * 128 + 16 * i + r16;
-        arow[i] = wm * 128 + 16 * i + r16;
-    }
+    for (int i = 0; i < 8; i++) wrow[i] = wn * 128 + 16 * i + r16;
+#pragma unroll
+    for (int j = 0; j < MJ; j++) arow[j] = wm * 16 * MJ + 16 * j + r16;
     // fragments of one k32 sub-step: eight 16-row blocks of W and of A (lane:
     // row r16 of the block, k 8 q .. 8 q + 7 of the sub-step)
-    bf16x8 wf[2][8], af[2][8];
+    bf16x8 wf[2][8], af[2][MJ];
     // slot `slot`, k32 sub-step s, fragment buffer buf
     auto read_frags = [&](int slot, int s, int buf) __attribute__((always_inline)) {
         const uint16_t* ws = lds + slot * STAGE_E;
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             wf[buf][i] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[i], 4 * s + q));
-            af[buf][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 4 * s + q));
+            if (i < MJ) af[buf][i] = *reinterpret_cast<const bf16x8*>(as + swz(arow[i], 4 * s + q));
         }
     };
     // One k32 sub-step: the 64 MFMAs on fragment buffer `buf`; in the first
@@ -271,16 +273,17 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
         const uint16_t* ws = lds + rslot * STAGE_E;
         const uint16_t* as = ws + BN * ROW_E;
 #pragma unroll
-        for (int g = 0; g < 64; g++) {
-            const int i = g >> 3, j = g & 7;
+        for (int g = 0; g < 8 * MJ; g++) {
+            const int i = g / MJ, j = g % MJ;
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (g < 32) {
                 if (dma && (g & 1)) load_piece(dma_kt, dma_slot, g >> 1);
                 if (do_read && !(g & 1)) {
                     const int r = g >> 2;
-                    if (g & 2)
-                        af[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(as + swz(arow[r], 4 * rs + q));
+                    if (g & 2) {
+                        if (r < MJ) af[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(as + swz(arow[r], 4 * rs + q));
+                    }
                     else
                         wf[buf ^ 1][r] = *reinterpret_cast<const bf16x8*>(ws + swz(wrow[r], 4 * rs + q));
                 }
@@ -317,29 +320,53 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the redundant last refill
     // every wave is done with the operand tiles: LDS becomes the staging area
     __syncthreads();
-    epilogue<EPI>(p, acc, n0 + wn * 128, m0 + wm * 128, lane, lds + wave * (128 * 128));
+    epilogue<EPI, MJ>(p, acc, n0 + wn * 128, m0 + wm * 16 * MJ, lane, lds + wave * (128 * 128));
 }
 
 }  // namespace
 
+// Tiles of 256 x 256 or 256 x 224 (rows of A), whichever needs fewer
+// workgroup rounds times rows per tile on the device's CUs: with 5498 rows,
+// 2560 output features give 220 tiles of 256 rows (1 round, 36 CUs idle) or
+// 250 of 224 (1 round, 12 % less work per tile).
 hipError_t launch_gemm(int epi, GemmBatch& b, hipStream_t s) {
+    static int n_cu[64] = {};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && n_cu[dev] == 0)
+        (void)hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev);
+    const int cus = (dev >= 0 && dev < 64 && n_cu[dev] > 0) ? n_cu[dev] : 256;
+    auto tiles_for = [&](int bm) {
+        long t = 0;
+        for (int i = 0; i < b.nprob; i++) t += (long)(b.p[i].N / BN) * ((b.p[i].M + bm - 1) / bm);
+        return t;
+    };
+    const long t8 = tiles_for(256), t7 = tiles_for(224);
+    const int mj = ((t7 + cus - 1) / cus) * 7 < ((t8 + cus - 1) / cus) * 8 ? 7 : 8;
+    const int bm = 32 * mj;
     b.total_tiles = 0;
     for (int i = 0; i < b.nprob; i++) {
         GemmProblem& p = b.p[i];
         p.n_tiles = p.N / BN;
-        p.m_tiles = (p.M + BM - 1) / BM;
+        p.m_tiles = (p.M + bm - 1) / bm;
         if (i == 0) b.tiles0 = p.n_tiles * p.m_tiles;
         b.total_tiles += p.n_tiles * p.m_tiles;
     }
     if (b.nprob == 1) b.p[1] = b.p[0];
     if (b.total_tiles == 0) return hipSuccess;
     const int grid = ((b.total_tiles + 7) >> 3) << 3;
+#define GEMM_LAUNCH(E)                                                                  \
+    do {                                                                                \
+        if (mj == 7) hipLaunchKernelGGL((gemm_kernel<E, 7>), dim3(grid), dim3(256), 0, s, b); \
+        else hipLaunchKernelGGL((gemm_kernel<E, 8>), dim3(grid), dim3(256), 0, s, b);         \
+    } while (0)
     switch (epi) {
-        case EPI_STORE: hipLaunchKernelGGL(gemm_kernel<EPI_STORE>, dim3(grid), dim3(256), 0, s, b); break;
-        case EPI_RESID: hipLaunchKernelGGL(gemm_kernel<EPI_RESID>, dim3(grid), dim3(256), 0, s, b); break;
-        case EPI_SWIGLU: hipLaunchKernelGGL(gemm_kernel<EPI_SWIGLU>, dim3(grid), dim3(256), 0, s, b); break;
+        case EPI_STORE: GEMM_LAUNCH(EPI_STORE); break;
+        case EPI_RESID: GEMM_LAUNCH(EPI_RESID); break;
+        case EPI_SWIGLU: GEMM_LAUNCH(EPI_SWIGLU); break;
         default: return hipErrorInvalidValue;
     }
+#undef GEMM_LAUNCH
     return hipGetLastError();
 }
 
