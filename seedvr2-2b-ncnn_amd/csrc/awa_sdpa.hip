@@ -798,6 +798,20 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                                           (size_t)cur.h * HEAD_D);
                 }
             } else {
+                // all token lookups (first, so that their round trips through
+                // LDS overlap the staging), then all row reads, then all stores:
+                // each group waits once.  Padding rows (token -1) get an offset
+                // past the buffer's end, which the buffer store drops, so no
+                // lane branches around its store.
+                const __amdgpu_buffer_rsrc_t ores =
+                    __builtin_amdgcn_make_buffer_rsrc(a.vattn, 0, a.vattn_bytes, 0x00020000);
+                const uint32_t col = 2 * ((uint32_t)cur.h * HEAD_D + (lane & 15) * 8);
+                uint32_t ofs[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int tok = __shfl(orow_cur[i >> 3], (4 * i + (lane >> 4)) & 31);
+                    ofs[i] = tok >= 0 ? (uint32_t)tok * (2 * DIM) + col : 0x80000000u;
+                }
                 uint16_t* stg = lds + (wave == 0 ? (kb + nk - 1) % 3 : 3 + ((vb + nk - 1) & 1)) * KT_E;
 #pragma unroll
                 for (int qb = 0; qb < 2; qb++) {
@@ -814,19 +828,6 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                             const int c = 4 * dt + g;
                             *reinterpret_cast<uint2*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3) + 4 * hb) = u;
                         }
-                }
-                // all token lookups, then all row reads, then all stores: each
-                // group waits once.  Padding rows (token -1) get an offset past
-                // the buffer's end, which the buffer store drops, so no lane
-                // branches around its store.
-                const __amdgpu_buffer_rsrc_t ores =
-                    __builtin_amdgcn_make_buffer_rsrc(a.vattn, 0, a.vattn_bytes, 0x00020000);
-                const uint32_t col = 2 * ((uint32_t)cur.h * HEAD_D + (lane & 15) * 8);
-                uint32_t ofs[16];
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int tok = __shfl(orow_cur[i >> 3], (4 * i + (lane >> 4)) & 31);
-                    ofs[i] = tok >= 0 ? (uint32_t)tok * (2 * DIM) + col : 0x80000000u;
                 }
                 u32x4 v[16];
 #pragma unroll
