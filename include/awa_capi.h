@@ -82,7 +82,10 @@ int awa_plan_windows(int t, int h, int w, const int32_t num_windows[3], int shif
 /* awa::make_win(t, h, w, num_windows, txt_len, shifted) followed by the index
  * build, on the device: window slices (unshifted or half-window shifted),
  * cumf, vidx and the RoPE frequency tables in the reference's formats.
- * Built once per resolution and reused (dit_graph.cpp:226-229 caches it). */
+ * Built once per resolution and reused (dit_graph.cpp:226-229 caches it).
+ * Every geometry entry point rejects (AWA_EARG) more than 559,240 video or
+ * text rows: the geometry's row table holds 32-bit element offsets into the
+ * 7680-wide projection rows (the bf16 op further accepts at most 279,620). */
 int awa_geom_build(awa_ctx* ctx, int t, int h, int w, const int32_t num_windows[3],
                    int txt_len, int shifted, awa_geom** out, awa_stream_t stream);
 

@@ -34,6 +34,7 @@
 //   EPI_STORE     C = bf16(acc)                               (qkv)
 //   EPI_RESID     X += gate[n] * (acc + bias[n]), X fp32      (out proj, MLP out)
 //   EPI_SWIGLU    U = bf16(silu(g) * h), W rows interleaved   (proj_in + proj_in_gate)
+#include <atomic>
 #include <type_traits>
 
 #include "dit_internal.hpp"
@@ -330,12 +331,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
 // 2560 output features give 220 tiles of 256 rows (1 round, 36 CUs idle) or
 // 250 of 224 (1 round, 12 % less work per tile).
 hipError_t launch_gemm(int epi, GemmBatch& b, hipStream_t s) {
-    static int n_cu[64] = {};
-    int dev = 0;
+    // CU count per device, looked up once (threads may race to store the same value)
+    static std::atomic<int> n_cu[64];
+    int dev = 0, cus = 256;
     (void)hipGetDevice(&dev);
-    if (dev >= 0 && dev < 64 && n_cu[dev] == 0)
-        (void)hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev);
-    const int cus = (dev >= 0 && dev < 64 && n_cu[dev] > 0) ? n_cu[dev] : 256;
+    if (dev >= 0 && dev < 64) {
+        int c = n_cu[dev].load(std::memory_order_relaxed);
+        if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+            n_cu[dev].store(c, std::memory_order_relaxed);
+        if (c > 0) cus = c;
+    }
     auto tiles_for = [&](int bm) {
         long t = 0;
         for (int i = 0; i < b.nprob; i++) t += (long)(b.p[i].N / BN) * ((b.p[i].M + bm - 1) / bm);
