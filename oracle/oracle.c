@@ -1,7 +1,7 @@
 /*
  * oracle.c — CPU restatement of the SeedVR2 AWA path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP implementation.  Only
+ * TEST INFRASTRUCTURE ONLY: the oracle the HIP implementation is tested against.  Only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it; the
  * product (seedvr2-2b-ncnn_amd/) never does.
  *

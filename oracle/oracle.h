@@ -1,7 +1,7 @@
 /*
  * oracle.h — CPU restatement of the SeedVR2 AWA path (TEST INFRASTRUCTURE ONLY).
  *
- * This library is the checker for the HIP implementation.  Only tests/,
+ * This library is the oracle the HIP implementation is tested against.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
  * product path (seedvr2-2b-ncnn_amd/) never links or calls it.
  *

@@ -154,7 +154,7 @@ def sdpa_asm(tmp_path_factory):
     return open(out).read()
 
 
-def test_checker_finds_planted_uses(sdpa_asm):
+def test_analysis_finds_planted_uses(sdpa_asm):
     insts = parse(sdpa_asm)
     k = next(i for i, (lab, op, rest) in enumerate(insts)
              if op and VMEM_LOAD.match(op) and rest.startswith("a"))
