@@ -19,6 +19,7 @@ namespace awa {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // The key/query tile sequence of one window: its video tiles, then the text
 // tiles of its text set.
@@ -155,31 +156,32 @@ void sdpa_f32_kernel(SdpaArgs a) {
     // other: K of the next tile is loaded at the top of an iteration and
     // stored to the free LDS stage after the score MFMAs, V is loaded then
     // and stored at the end (two staging sets at once made the kernel spill).
-    float4 reg[8];
-    auto load_k = [&](int kk) {
-        const float4* src = reinterpret_cast<const float4*>(Kh + (size_t)wt.tile(kk) * TILE * HEAD_D);
+    // (a plain vector type: an array of HIP's float4 stayed in scratch memory)
+    f32x4 reg[8];
+    auto load_k = [&](int kk) __attribute__((always_inline)) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(Kh + (size_t)wt.tile(kk) * TILE * HEAD_D);
 #pragma unroll
         for (int i = 0; i < 8; i++) reg[i] = src[tid + 256 * i];
     };
-    auto load_v = [&](int kk) {
-        const float4* src = reinterpret_cast<const float4*>(Vh + (size_t)wt.tile(kk) * TILE * HEAD_D);
+    auto load_v = [&](int kk) __attribute__((always_inline)) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(Vh + (size_t)wt.tile(kk) * TILE * HEAD_D);
 #pragma unroll
         for (int i = 0; i < 8; i++) reg[i] = src[tid + 256 * i];
     };
-    auto store_k = [&](int stage) {
+    auto store_k = [&](int stage) __attribute__((always_inline)) {
         float* ks = lds + stage * STAGE32;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<float4*>(ks + (c >> 5) * KP32 + (c & 31) * 4) = reg[i];
+            *reinterpret_cast<f32x4*>(ks + (c >> 5) * KP32 + (c & 31) * 4) = reg[i];
         }
     };
-    auto store_v = [&](int stage) {
+    auto store_v = [&](int stage) __attribute__((always_inline)) {
         float* vs = lds + stage * STAGE32 + KS32;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<float4*>(vs + (c >> 4) * VP32 + (c & 15) * 4) = reg[i];
+            *reinterpret_cast<f32x4*>(vs + (c >> 4) * VP32 + (c & 15) * 4) = reg[i];
         }
     };
 
