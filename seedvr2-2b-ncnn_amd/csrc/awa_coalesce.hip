@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void cast_f32_bf16_kernel(const float* __restr
                                                             uint16_t* __restrict__ out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t j = i; j < n; j += stride) out[j] = (uint16_t)bf16_rne(in[j]);
+    for (int64_t j = i; j < n; j += stride) out[j] = (uint16_t)bf16x2_rne(in[j], 0.f);
 }
 
 __global__ __launch_bounds__(256) void cast_bf16_f32_kernel(const uint16_t* __restrict__ in,

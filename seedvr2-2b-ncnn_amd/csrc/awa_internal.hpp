@@ -46,6 +46,17 @@ __device__ inline uint32_t bf16_rne(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
+// Two floats -> two bf16 in one word (lo in the low half) by the hardware
+// conversion (one v_cvt_pk_bf16_f32 where bf16_rne takes four instructions per
+// value).  Equal to bf16_rne on every finite value: awa_cast_f32_to_bf16 uses
+// it and is checked against torch's cast on all finite patterns and against
+// the integer formula on a sample (NaNs stay NaNs here, which the formula can
+// turn into infinities).
+__device__ inline uint32_t bf16x2_rne(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
 
 // Integer restatement of awa_window.cpp:15-78 along one axis.  The reference
 // forms shifted bounds as int((i - 0.5) * wX) in double; for integer i and wX

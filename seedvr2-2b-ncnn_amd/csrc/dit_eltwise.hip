@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void norm_ada_kernel(NormArgs a) {
             o2 = o2 * s.z + t.z;
             o3 = o3 * s.w + t.w;
         }
-        out[i * 64 + lane] = make_uint2(bf16_rne(o0) | (bf16_rne(o1) << 16), bf16_rne(o2) | (bf16_rne(o3) << 16));
+        out[i * 64 + lane] = make_uint2(bf16x2_rne(o0, o1), bf16x2_rne(o2, o3));
     }
 }
 

@@ -83,8 +83,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const f32x4& a = acc[i][j];
-                const uint2 u = make_uint2(bf16_rne(a[0]) | (bf16_rne(a[1]) << 16),
-                                           bf16_rne(a[2]) | (bf16_rne(a[3]) << 16));
+                const uint2 u = make_uint2(bf16x2_rne(a[0], a[1]), bf16x2_rne(a[2], a[3]));
                 const int c = 2 * i + (q >> 1);
                 *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ (r & 15)) << 3) + 4 * (q & 1)) = u;
             }
@@ -118,7 +117,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
                             const float gt = acc[4 * h + 2 + e][j][t2 + t];
                             o[t] = gt / (1.f + __expf(-gt)) * hv;
                         }
-                        packed[t2 >> 1] = bf16_rne(o[0]) | (bf16_rne(o[1]) << 16);
+                        packed[t2 >> 1] = bf16x2_rne(o[0], o[1]);
                     }
                     const int c = 4 * h + 2 * e + (q >> 1);
                     *reinterpret_cast<uint2*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3) + 4 * (q & 1)) =
