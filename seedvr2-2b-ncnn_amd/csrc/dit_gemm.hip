@@ -235,11 +235,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
         for (int g = 0; g < 16; g++) load_piece(kt, slot, g);
     };
 
+    // no zero fill: the first sub-step's MFMAs take a zero accumulator operand
     f32x4 acc[8][MJ];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int j = 0; j < MJ; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int nk = p.K / BK;
     int wrow[8], arow[MJ];
@@ -268,14 +265,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     // previous sub-step's reads comes before the first new read (the compiler
     // waits on the LDS counter with lgkmcnt(0)), and the DMA pieces go out
     // early, which leaves them a sub-step and a half to land.
-    auto substep = [&](int buf, int rslot, int rs, bool do_read, bool dma, int dma_kt, int dma_slot)
+    auto substep = [&](int buf, int rslot, int rs, bool do_read, bool dma, int dma_kt, int dma_slot, bool zc)
         __attribute__((always_inline)) {
         const uint16_t* ws = lds + rslot * STAGE_E;
         const uint16_t* as = ws + BN * ROW_E;
 #pragma unroll
         for (int g = 0; g < 8 * MJ; g++) {
             const int i = g / MJ, j = g % MJ;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][i], af[buf][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                wf[buf][i], af[buf][j], zc ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (g < 32) {
                 if (dma && (g & 1)) load_piece(dma_kt, dma_slot, g >> 1);
@@ -308,15 +306,26 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmBatch b) {
     __builtin_amdgcn_s_barrier();
     read_frags(0, 0, 0);
     int slot = 0;
-    for (int kt = 0; kt < last; kt++) {
-        substep(0, slot, 1, true, false, 0, 0);
+    if (last == 0) {  // one K stage
+        substep(0, 0, 1, true, false, 0, 0, true);
+        substep(1, 0, 0, false, false, 0, 0, false);
+    } else {
+        // stage 0 peeled: its first sub-step starts the accumulators
+        substep(0, 0, 1, true, false, 0, 0, true);
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        substep(1, slot ^ 1, 0, true, true, min(kt + 2, last), slot);
-        slot ^= 1;
+        substep(1, 1, 0, true, true, min(2, last), 0, false);
+        slot = 1;
+        for (int kt = 1; kt < last; kt++) {
+            substep(0, slot, 1, true, false, 0, 0, false);
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            substep(1, slot ^ 1, 0, true, true, min(kt + 2, last), slot, false);
+            slot ^= 1;
+        }
+        substep(0, slot, 1, true, false, 0, 0, false);
+        substep(1, slot, 0, false, false, 0, 0, false);
     }
-    substep(0, slot, 1, true, false, 0, 0);
-    substep(1, slot, 0, false, false, 0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the redundant last refill
     // every wave is done with the operand tiles: LDS becomes the staging area
     __syncthreads();
