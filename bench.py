@@ -120,13 +120,18 @@ def config_runs(ctx, torch, steps, cpu=True):
         for _ in range(3):
             ctx.forward(g, vq, tq, *gains, eps=1e-5, vattn=va, tattn=ta)
         torch.cuda.synchronize()
-        ctx.timing(True)
-        ctx.timing_read()
+        # wall clock with per-phase events off, then the phases in a pass of
+        # their own (the events add work to every call)
         t0 = time.perf_counter()
         for _ in range(steps):
             ctx.forward(g, vq, tq, *gains, eps=1e-5, vattn=va, tattn=ta)
         torch.cuda.synchronize()
         layer_ms = (time.perf_counter() - t0) * 1e3 / steps
+        ctx.timing(True)
+        ctx.timing_read()
+        for _ in range(steps):
+            ctx.forward(g, vq, tq, *gains, eps=1e-5, vattn=va, tattn=ta)
+        torch.cuda.synchronize()
         mp, ma, mt, c = ctx.timing_read()
         ctx.timing(False)
         es = 4 if store == "f32" else 2

@@ -154,7 +154,7 @@ void plan_schedule(GeomPlan& P, int n_slots) {
     P.n_slots = n_slots;
     const int per_xcd = n_slots / XCDS;
     std::vector<int> win_cost(P.nwin);
-    for (int w = 0; w < P.nwin; w++) win_cost[w] = 10 * (P.tile_base[w + 1] - P.tile_base[w] + P.ntt) + 25;
+    for (int w = 0; w < P.nwin; w++) win_cost[w] = 10 * stream_tiles(P.tile_base[w + 1] - P.tile_base[w], P.ntt) + 25;
     struct Group { long cost; int h, w; };
     std::vector<Group> groups;
     std::vector<std::vector<int>> items_of(P.nwin);

@@ -140,6 +140,30 @@ constexpr long VROW_MAX_OFFSET_ROWS = 0xffffffffL / QKV;
 constexpr long VROW_MAX_ROWS = 0xffffffffL / (2L * QKV);
 __host__ __device__ inline int vrow_pos(int r) { return 32 * (r >> 5) + 8 * (r & 3) + ((r & 31) >> 2); }
 
+// The key tiles of the bf16 attention kernel's DMA stream.  A slot's stream
+// is the key tiles of its work items in order: a window's nvt video tiles,
+// then the ntt text tiles.  Tile kk of an item fetches K tile kk + 2 and V
+// tile kk + 1 of the stream, so past the item's end the next item's first
+// two tiles; for that every item must hold at least two tiles.  A window
+// without video rows and at most 64 text rows (possible for injected
+// geometry) has one: it gets a second that repeats its last text tile, whose
+// keys all lie past the text and are masked.
+__host__ __device__ inline int stream_tiles(int nvt, int ntt) { return nvt + ntt > 2 ? nvt + ntt : 2; }
+// Tile index of key tile kk (< stream_tiles) of an item: video tiles from
+// vbase, text tiles from tbase (packed K: the window's text set; V row
+// table: n_vid_tiles), clamped to the last text tile.
+__host__ __device__ inline int stream_tile(int kk, int nvt, int vbase, int tbase, int ntt) {
+    return kk < nvt ? vbase + kk : tbase + (kk - nvt < ntt - 1 ? kk - nvt : ntt - 1);
+}
+// The fetch of key tile kk of an item with nk stream tiles: K tile k_kk and
+// V tile v_kk of the current item (*_nxt = 0) or of the next one (*_nxt = 1).
+__host__ __device__ inline void stream_fetch(int kk, int nk, int* k_kk, int* k_nxt, int* v_kk, int* v_nxt) {
+    *k_nxt = kk + 2 >= nk;
+    *k_kk = *k_nxt ? kk + 2 - nk : kk + 2;
+    *v_nxt = kk + 1 >= nk;
+    *v_kk = *v_nxt ? kk + 1 - nk : kk + 1;
+}
+
 }  // namespace awa
 
 struct awa_ctx {

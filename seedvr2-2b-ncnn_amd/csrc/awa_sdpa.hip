@@ -399,12 +399,12 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lptr_t)lds;
     // tile index of key tile kk of work item W (packed K)
     auto tile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
-        return kk < W.nvt ? W.vbase + kk : W.tbase + (kk - W.nvt);
+        return stream_tile(kk, W.nvt, W.vbase, W.tbase, a.ntt);
     };
     // The DMA stream of a slot is the key tiles of its items in order: tile kk
     // of an item fetches K tile kk + 2 and V^T tile kk + 1 of the stream, which
-    // past the item's end are the next item's first tiles (an item has at
-    // least two key tiles, one of them text).  Past the slot's last item a
+    // past the item's end are the next item's first tiles (stream_fetch; an
+    // item has at least two key tiles, stream_tiles).  Past the slot's last item a
     // tile fetches its own tile again into the free slot, so that every tile
     // issues the same instructions (the kernel waits for these before it
     // ends; those fetches get empty buffers, whose loads write zeros without
@@ -434,7 +434,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
     u32x4 vt0, vt1;
     uint32_t vo[8];
     auto vtile_of = [&](const Work& W, int kk) __attribute__((always_inline)) {
-        return kk < W.nvt ? W.vbase + kk : a.n_vid_tiles + (kk - W.nvt);
+        return stream_tile(kk, W.nvt, W.vbase, a.n_vid_tiles, a.ntt);
     };
     auto load_vt = [&](int vtile) __attribute__((always_inline)) {
         const u32x4* p = reinterpret_cast<const u32x4*>(a.vrow + (size_t)vtile * TILE + wave * 32 + (lane >> 4) * 8);
@@ -532,7 +532,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         const bool has_next = wi + 1 < wi1;
         const Work nxt = load_work(desc, has_next ? wi + 1 : wi);
         const int orow_cur[2] = {orow[0], orow[1]};
-        const int nk = cur.nvt + a.ntt;
+        const int nk = stream_tiles(cur.nvt, a.ntt);
         const int kq = wave == 0 ? cur.q0 : cur.q1;
         const bool active = kq >= 0;
         auto nvalid = [&](int kk) __attribute__((always_inline)) {
@@ -732,25 +732,27 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             // stream) and the V^T tile of the next tile's fetch
             // (values, not a choice between the two items' fields: a
             // conditional lvalue keeps both items in scratch memory)
+            int k_kk, k_nxt, v_kk, v_nxt;
+            stream_fetch(kk, nk, &k_kk, &k_nxt, &v_kk, &v_nxt);
             int kh = cur.h, kt = tile_of(cur, kk), vh = cur.h;
             bool vtxt = kk >= cur.nvt;
             nv_tile = vtile_of(cur, min(kk + 1, nk - 1));
-            if (kk + 2 < nk) {
-                kt = tile_of(cur, kk + 2);
-                nv_tile = vtile_of(cur, kk + 2);
+            if (!k_nxt) {
+                kt = tile_of(cur, k_kk);
+                nv_tile = vtile_of(cur, k_kk);
             } else if (has_next) {
                 kh = nxt.h;
-                kt = tile_of(nxt, kk + 2 - nk);
-                nv_tile = vtile_of(nxt, kk + 2 - nk);
+                kt = tile_of(nxt, k_kk);
+                nv_tile = vtile_of(nxt, k_kk);
             }
-            if (kk + 1 < nk) {
-                vtxt = kk + 1 >= cur.nvt;
+            if (!v_nxt) {
+                vtxt = v_kk >= cur.nvt;
             } else if (has_next) {
                 vh = nxt.h;
-                vtxt = 0 >= nxt.nvt;
+                vtxt = v_kk >= nxt.nvt;
             }
-            set_k(kh, kt, (kb + kk + 2) % 3, kk + 2 < nk || has_next);
-            set_v(vh, vtxt, (vb + kk + 1) & 1, kk + 1 < nk || has_next);
+            set_k(kh, kt, (kb + kk + 2) % 3, !k_nxt || has_next);
+            set_v(vh, vtxt, (vb + kk + 1) & 1, !v_nxt || has_next);
             prep_v();
             if (active) {
                 unit(2 * kk, true, true);

@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
+#include <cstdint>
+#include <exception>
 #include <sstream>
 
 #include "dit_files.hpp"
@@ -69,6 +71,9 @@ bool tagged_bytes(uint32_t tag, int64_t n, int64_t* bytes) {
 // n values of a "type 0" blob at byte off of f (the tag first).
 int read_tagged_at(std::ifstream& f, int64_t size, int64_t off, int64_t n, const std::string& what,
                    std::vector<float>& v) {
+    if (n < 0 || off < 0 || off > size - 4 || n > (size - off - 4) / 2)
+        return fail("%s: %lld values at byte %lld exceed the %lld-byte file", what.c_str(), (long long)n,
+                    (long long)off, (long long)size);
     uint32_t tag = 0;
     f.clear();
     f.seekg(off);
@@ -135,6 +140,8 @@ int read_linear_host(const std::string& base, bool has_bias, HostLinear& L) {
     }
     if (numout <= 0 || total <= 0 || total % numout)
         return fail("%s.param: no InnerProduct line with 0=num_output and 2=weight_data_size", base.c_str());
+    if (numout > INT32_MAX || total / numout > INT32_MAX)
+        return fail("%s.param: InnerProduct 0=%ld 2=%ld out of range", base.c_str(), numout, total);
     std::ifstream bf(base + ".bin", std::ios::binary);
     if (!bf) return fail("cannot open %s.bin", base.c_str());
     int64_t size;
@@ -258,6 +265,11 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
     // a tagged blob of n values at off: its extent
     auto tagged = [&](const std::string& name, int64_t n, const std::string& layer) -> int {
         if (n <= 0) return fail("%s: layer %s: a blob of %lld values", param.c_str(), layer.c_str(), (long long)n);
+        // at least 2 bytes per value (fp16) after the 4-byte tag: bound n
+        // before any size arithmetic
+        if (off > G.bin_size - 4 || n > (G.bin_size - off - 4) / 2)
+            return fail("%s: layer %s: %lld values exceed the %lld bytes of %s", param.c_str(), layer.c_str(),
+                        (long long)n, (long long)G.bin_size, bin.c_str());
         uint32_t tag = 0;
         f.clear();
         f.seekg(off);
@@ -276,7 +288,7 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
         if (t == "Input" || t == "BinaryOp" || t == "Swish" || t == "Cast" || t == "Split" || t == "Noop") continue;
         if (t == "InnerProduct") {
             const long nout = L.geti(0, 0), bias = L.geti(1, 0), total = L.geti(2, 0);
-            if (nout <= 0 || total <= 0 || total % nout)
+            if (nout <= 0 || total <= 0 || total % nout || nout > INT32_MAX || total / nout > INT32_MAX)
                 return fail("%s: InnerProduct %s: 0=%ld 2=%ld", param.c_str(), L.name.c_str(), nout, total);
             std::string name, kind;
             int i;
@@ -292,6 +304,9 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
             if (name.empty()) return fail("%s: unknown InnerProduct layer %s", param.c_str(), L.name.c_str());
             const int64_t start = off;
             if (tagged("", total, L.name)) return -1;
+            if (bias && nout > (G.bin_size - off) / 4)
+                return fail("%s: %lld bytes end inside the bias of %s", bin.c_str(), (long long)G.bin_size,
+                            L.name.c_str());
             off += bias ? 4 * nout : 0;
             add(name, GraphBlob{GraphBlob::LINEAR, start, total, (int)nout, (int)(total / nout), bias != 0});
         } else if (t == "AWA") {
@@ -306,7 +321,7 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
             for (const char* nm : {"_nq", "_nk"}) if (tagged(branch(i, 't') + nm, 128, L.name)) return -1;
         } else if (t == "AdaCompose") {
             const long nl = L.geti(1, 32), dim = L.geti(3, 2560), fin = L.geti(4, 1);
-            if (nl < 0 || nl > 4096 || dim <= 0)
+            if (nl < 0 || nl > 4096 || dim <= 0 || dim > INT32_MAX)
                 return fail("%s: AdaCompose %s: 1=%ld 3=%ld", param.c_str(), L.name.c_str(), nl, dim);
             for (int i = 0; i < nl; i++)
                 for (char fl : {'v', 't'})
@@ -318,7 +333,9 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
         } else if (t == "RMSNorm") {
             if (L.geti(2, 0)) {
                 const long n = L.geti(0, 0);
-                if (n <= 0) return fail("%s: RMSNorm %s: 0=%ld", param.c_str(), L.name.c_str(), n);
+                if (n <= 0 || n > (G.bin_size - off) / 4)
+                    return fail("%s: RMSNorm %s: 0=%ld values past the end of %s", param.c_str(), L.name.c_str(), n,
+                                bin.c_str());
                 if (L.name == "rn_fin") add("vid_out_norm_w", GraphBlob{GraphBlob::RAW, off, n, (int)n, 0, false});
                 off += 4 * n;
             }
@@ -340,99 +357,127 @@ int index_graph(const std::string& param, const std::string& bin, int mm_hint, G
 
 using namespace dit_files;
 
+namespace {
+
+// Runs a reader body; an exception (bad_alloc of a huge but well-formed
+// request, a stream error) becomes a -1 return with its message, never a
+// throw across the C ABI.
+template <typename F>
+int guarded(const char* who, F&& body) {
+    try {
+        return body();
+    } catch (const std::exception& e) {
+        return fail("%s: %s", who, e.what());
+    } catch (...) {
+        return fail("%s: unknown exception", who);
+    }
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* dit_host_last_error(void) { return last_error().c_str(); }
 void dit_free_host(void* p) { std::free(p); }
 
 int dit_read_raw_f(const char* path, float** data, int64_t* count, int64_t shape[8], int* ndim) {
-    if (!path || !data || !count) return fail("dit_read_raw_f: null argument");
-    std::vector<float> d;
-    std::vector<int64_t> sh;
-    if (read_raw_host(path, d, sh)) return -1;
-    *data = copy_out(d);
-    *count = (int64_t)d.size();
-    if (ndim) *ndim = (int)sh.size();
-    if (shape)
-        for (size_t i = 0; i < sh.size(); i++) shape[i] = sh[i];
-    return 0;
+    return guarded("dit_read_raw_f", [&]() -> int {
+        if (!path || !data || !count) return fail("dit_read_raw_f: null argument");
+        std::vector<float> d;
+        std::vector<int64_t> sh;
+        if (read_raw_host(path, d, sh)) return -1;
+        *data = copy_out(d);
+        *count = (int64_t)d.size();
+        if (ndim) *ndim = (int)sh.size();
+        if (shape)
+            for (size_t i = 0; i < sh.size(); i++) shape[i] = sh[i];
+        return 0;
+    });
 }
 
 int dit_read_linear(const char* base, int has_bias, float** w, float** b, int* n_out, int* n_in) {
-    if (!base || !w) return fail("dit_read_linear: null argument");
-    HostLinear L;
-    if (read_linear_host(base, has_bias != 0, L)) return -1;
-    *w = copy_out(L.w);
-    if (b) *b = has_bias ? copy_out(L.b) : nullptr;
-    if (n_out) *n_out = L.n_out;
-    if (n_in) *n_in = L.n_in;
-    return 0;
+    return guarded("dit_read_linear", [&]() -> int {
+        if (!base || !w) return fail("dit_read_linear: null argument");
+        HostLinear L;
+        if (read_linear_host(base, has_bias != 0, L)) return -1;
+        *w = copy_out(L.w);
+        if (b) *b = has_bias ? copy_out(L.b) : nullptr;
+        if (n_out) *n_out = L.n_out;
+        if (n_in) *n_in = L.n_in;
+        return 0;
+    });
 }
 
 int dit_read_win(const char* path, int txt_len, int64_t header[10], int32_t** slices, float** vid_freq,
                  int64_t* n_vid, float** txt_freq, int64_t* n_txt) {
-    if (!path || !header || !slices || !vid_freq || !txt_freq || txt_len < 0)
-        return fail("dit_read_win: bad argument");
-    std::ifstream f(path, std::ios::binary);
-    if (!f) return fail("cannot open %s", path);
-    int64_t size;
-    file_size(f, &size);
-    f.read(reinterpret_cast<char*>(header), 80);
-    const int64_t nwin = header[9];
-    if (!f || nwin < 1 || nwin > 4096) return fail("%s: bad header (nwin %lld)", path, (long long)nwin);
-    std::vector<int64_t> sl(nwin * 6);
-    f.read(reinterpret_cast<char*>(sl.data()), nwin * 48);
-    const int64_t nf = (size - 80 - nwin * 48) / 4;
-    const int64_t nt = nwin * txt_len * 126;
-    if (!f || nf < nt || (nf - nt) % 126)
-        return fail("%s: %lld floats do not split into vid_freq and %lld txt_freq floats", path, (long long)nf,
-                    (long long)nt);
-    std::vector<float> all(nf);
-    f.read(reinterpret_cast<char*>(all.data()), nf * 4);
-    if (!f) return fail("%s: read error", path);
-    std::vector<int32_t> s32(sl.begin(), sl.end());
-    *slices = copy_out(s32);
-    *vid_freq = copy_out(std::vector<float>(all.begin(), all.end() - nt));
-    *txt_freq = copy_out(std::vector<float>(all.end() - nt, all.end()));
-    if (n_vid) *n_vid = nf - nt;
-    if (n_txt) *n_txt = nt;
-    return 0;
+    return guarded("dit_read_win", [&]() -> int {
+        if (!path || !header || !slices || !vid_freq || !txt_freq || txt_len < 0)
+            return fail("dit_read_win: bad argument");
+        std::ifstream f(path, std::ios::binary);
+        if (!f) return fail("cannot open %s", path);
+        int64_t size;
+        file_size(f, &size);
+        f.read(reinterpret_cast<char*>(header), 80);
+        const int64_t nwin = header[9];
+        if (!f || nwin < 1 || nwin > 4096) return fail("%s: bad header (nwin %lld)", path, (long long)nwin);
+        std::vector<int64_t> sl(nwin * 6);
+        f.read(reinterpret_cast<char*>(sl.data()), nwin * 48);
+        const int64_t nf = (size - 80 - nwin * 48) / 4;
+        const int64_t nt = nwin * txt_len * 126;
+        if (!f || nf < nt || (nf - nt) % 126)
+            return fail("%s: %lld floats do not split into vid_freq and %lld txt_freq floats", path, (long long)nf,
+                        (long long)nt);
+        std::vector<float> all(nf);
+        f.read(reinterpret_cast<char*>(all.data()), nf * 4);
+        if (!f) return fail("%s: read error", path);
+        std::vector<int32_t> s32(sl.begin(), sl.end());
+        *slices = copy_out(s32);
+        *vid_freq = copy_out(std::vector<float>(all.begin(), all.end() - nt));
+        *txt_freq = copy_out(std::vector<float>(all.end() - nt, all.end()));
+        if (n_vid) *n_vid = nf - nt;
+        if (n_txt) *n_txt = nt;
+        return 0;
+    });
 }
 
 int dit_graph_file_info(const char* param, const char* bin, int mm_layers, int* n_layers, int* mm_out,
                         int* n_weights) {
-    if (!param || !bin) return fail("dit_graph_file_info: null argument");
-    GraphIndex G;
-    if (index_graph(param, bin, mm_layers, G)) return -1;
-    if (n_layers) *n_layers = G.n_layers;
-    if (mm_out) *mm_out = G.mm_layers;
-    if (n_weights) *n_weights = (int)G.w.size();
-    return 0;
+    return guarded("dit_graph_file_info", [&]() -> int {
+        if (!param || !bin) return fail("dit_graph_file_info: null argument");
+        GraphIndex G;
+        if (index_graph(param, bin, mm_layers, G)) return -1;
+        if (n_layers) *n_layers = G.n_layers;
+        if (mm_out) *mm_out = G.mm_layers;
+        if (n_weights) *n_weights = (int)G.w.size();
+        return 0;
+    });
 }
 
 int dit_read_graph_weight(const char* param, const char* bin, int mm_layers, const char* name, float** w,
                           float** b, int* n_out, int* n_in) {
-    if (!param || !bin || !name || !w) return fail("dit_read_graph_weight: null argument");
-    GraphSource src;
-    if (index_graph(param, bin, mm_layers, src.G) || src.open()) return -1;
-    const GraphBlob* g = src.find(name);
-    if (!g) return src.missing(name);
-    if (g->kind == GraphBlob::LINEAR) {
-        HostLinear L;
-        if (src.linear(name, g->bias, L)) return -1;
-        *w = copy_out(L.w);
-        if (b) *b = g->bias ? copy_out(L.b) : nullptr;
-        if (n_out) *n_out = L.n_out;
-        if (n_in) *n_in = L.n_in;
-    } else {
-        std::vector<float> v;
-        if (src.vec(name, v)) return -1;
-        *w = copy_out(v);
-        if (b) *b = nullptr;
-        if (n_out) *n_out = (int)v.size();
-        if (n_in) *n_in = 0;
-    }
-    return 0;
+    return guarded("dit_read_graph_weight", [&]() -> int {
+        if (!param || !bin || !name || !w) return fail("dit_read_graph_weight: null argument");
+        GraphSource src;
+        if (index_graph(param, bin, mm_layers, src.G) || src.open()) return -1;
+        const GraphBlob* g = src.find(name);
+        if (!g) return src.missing(name);
+        if (g->kind == GraphBlob::LINEAR) {
+            HostLinear L;
+            if (src.linear(name, g->bias, L)) return -1;
+            *w = copy_out(L.w);
+            if (b) *b = g->bias ? copy_out(L.b) : nullptr;
+            if (n_out) *n_out = L.n_out;
+            if (n_in) *n_in = L.n_in;
+        } else {
+            std::vector<float> v;
+            if (src.vec(name, v)) return -1;
+            *w = copy_out(v);
+            if (b) *b = nullptr;
+            if (n_out) *n_out = (int)v.size();
+            if (n_in) *n_in = 0;
+        }
+        return 0;
+    });
 }
 
 }  // extern "C"

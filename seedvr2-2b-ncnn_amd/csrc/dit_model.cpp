@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <fstream>
 #include <map>
+#include <exception>
 #include <memory>
 #include <sstream>
 #include <string>
@@ -109,9 +110,19 @@ int load_model_from(awa_ctx* ctx, WeightSource& src, int n_layers, int mm_layers
         }
         return p;
     };
+    // the readers return -1 on a bad file; an exception (memory exhausted by
+    // a huge but well-formed file) is turned into the same error
+    auto read_ok = [&](auto&& read) {
+        try {
+            return read() == 0;
+        } catch (const std::exception& e) {
+            fail("%s", e.what());
+            return false;
+        }
+    };
     auto linear = [&](const std::string& name, bool bias, int n_out, int n_in, HostLinear& L) {
         if (rc != AWA_OK) return false;
-        if (src.linear(name, bias, L)) {
+        if (!read_ok([&] { return src.linear(name, bias, L); })) {
             set_err(ctx, "dit_model_load: %s", last_error().c_str());
             rc = AWA_EARG;
             return false;
@@ -125,7 +136,7 @@ int load_model_from(awa_ctx* ctx, WeightSource& src, int n_layers, int mm_layers
     auto vec = [&](const std::string& name, size_t n) -> float* {
         if (rc != AWA_OK) return nullptr;
         std::vector<float> v;
-        if (src.vec(name, v)) {
+        if (!read_ok([&] { return src.vec(name, v); })) {
             set_err(ctx, "dit_model_load: %s", last_error().c_str());
             rc = AWA_EARG;
             return nullptr;
@@ -237,7 +248,13 @@ int dit_model_load_graph(awa_ctx* ctx, const char* param, const char* bin, const
     GraphSource src;
     std::unique_ptr<DirSource> d(dir ? new DirSource(dir) : nullptr);
     src.dir = d.get();
-    if (index_graph(param, bin, mm_layers, src.G) || src.open()) {
+    int bad_graph;
+    try {
+        bad_graph = index_graph(param, bin, mm_layers, src.G) || src.open();
+    } catch (const std::exception& e) {
+        bad_graph = fail("%s", e.what());
+    }
+    if (bad_graph) {
         set_err(ctx, "dit_model_load_graph: %s", last_error().c_str());
         return AWA_EARG;
     }

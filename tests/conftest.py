@@ -53,6 +53,19 @@ def metrics(out, ref):
     return cos, rel, md
 
 
+def rel_elementwise(out, ref, floor=1e-3):
+    """Elementwise relative error max |out - ref| / |ref| over the elements with
+    |ref| >= floor * max|ref| (below the floor a relative error measures
+    cancellation in the reference, not the result), and the count of such
+    elements."""
+    a = np.asarray(out, np.float64).ravel()
+    b = np.asarray(ref, np.float64).ravel()
+    big = np.abs(b) >= floor * np.max(np.abs(b))
+    if not big.any():
+        return 0.0, 0
+    return float(np.max(np.abs(a[big] - b[big]) / np.abs(b[big]))), int(big.sum())
+
+
 def seeded_awa_inputs(Lv, txt, seed, outlier_frac=0.0, outlier_scale=8.0):
     """q/k/v ~ N(0,1) rows [Lv,7680] / [txt,7680], gains 1 + N(0,0.02)."""
     rng = np.random.default_rng(seed)

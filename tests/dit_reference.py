@@ -32,9 +32,16 @@ def silu(v):
     return v / (np.float32(1.0) + np.exp(-v))
 
 
-def layer_emulation(O, x, emb, vb, tb, geom, Lv, TXT, last=False, eps=1e-5, bf16=True):
+def np_mm(a, w):
+    """a @ w.T in fp32 (numpy)."""
+    return a @ w.T
+
+
+def layer_emulation(O, x, emb, vb, tb, geom, Lv, TXT, last=False, eps=1e-5, bf16=True, mm=np_mm):
     """One layer on x [Lv+TXT, 2560] fp32; branches are dicts of fp32 numpy arrays with
-    keys qkv_w, out_w, out_b, mlp_in_w, mlp_g_w, mlp_out_w, nq, nk and the six ada vectors."""
+    keys qkv_w, out_w, out_b, mlp_in_w, mlp_g_w, mlp_out_w, nq, nk and the six ada vectors.
+    mm(a, w) computes the fp32 product a @ w.T (numpy by default; the full-size GPU
+    tests pass an fp32 device product to keep the CPU time of 1080p layers short)."""
     rnd = O.bf16_round if bf16 else (lambda a: np.asarray(a, np.float32))
     x = np.array(x, np.float32, copy=True)
     xv, xt = x[:Lv], x[Lv:]
@@ -44,20 +51,20 @@ def layer_emulation(O, x, emb, vb, tb, geom, Lv, TXT, last=False, eps=1e-5, bf16
     if not last:
         ht = ht * at["a_sc"] + at["a_sh"]
     ht = rnd(ht)
-    qv = rnd(hv @ vb["qkv_w"].T)
-    qt = rnd(ht @ tb["qkv_w"].T)
+    qv = rnd(mm(hv, vb["qkv_w"]))
+    qt = rnd(mm(ht, tb["qkv_w"]))
     va, ta = O.awa_forward(qv, qt, geom, vb["nq"], vb["nk"], tb["nq"], tb["nk"], eps=eps)
     va, ta = rnd(va), rnd(ta)
-    xv += av["a_g"] * (va @ vb["out_w"].T + vb["out_b"])
-    ot = ta @ tb["out_w"].T + tb["out_b"]
+    xv += av["a_g"] * (mm(va, vb["out_w"]) + vb["out_b"])
+    ot = mm(ta, tb["out_w"]) + tb["out_b"]
     xt += ot if last else at["a_g"] * ot
     hv = rnd(rmsnorm_rows(xv, eps) * av["m_sc"] + av["m_sh"])
-    uv = rnd(silu(hv @ vb["mlp_g_w"].T) * (hv @ vb["mlp_in_w"].T))
-    xv += av["m_g"] * (uv @ vb["mlp_out_w"].T)
+    uv = rnd(silu(mm(hv, vb["mlp_g_w"])) * mm(hv, vb["mlp_in_w"]))
+    xv += av["m_g"] * mm(uv, vb["mlp_out_w"])
     if not last:
         ht = rnd(rmsnorm_rows(xt, eps) * at["m_sc"] + at["m_sh"])
-        ut = rnd(silu(ht @ tb["mlp_g_w"].T) * (ht @ tb["mlp_in_w"].T))
-        xt += at["m_g"] * (ut @ tb["mlp_out_w"].T)
+        ut = rnd(silu(mm(ht, tb["mlp_g_w"])) * mm(ht, tb["mlp_in_w"]))
+        xt += at["m_g"] * mm(ut, tb["mlp_out_w"])
     return x
 
 

@@ -44,6 +44,66 @@ def test_last_layer_text_skips_mlp(oracle):
         assert np.array_equal(a[g.Lv:], b[g.Lv:]) == last
 
 
+ADA = ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate")
+
+
+@pytest.mark.parametrize("key", ADA)
+def test_last_layer_ignores_text_ada(oracle, key):
+    """forward_latent's last layer is vid_only (dit_vk.cpp:523-620): for the
+    text rows it skips the ada modulation before attention (:538), the
+    attention gate (:560), the MLP norm and ada (:579, :590) and the MLP with
+    its gate (:610, :617), so none of the text branch's six ada vectors may
+    change any output row; in a full layer each one changes the text rows.
+    Checked on the C oracle (orc_dit_layer, txt_vid_only = 1 / 0) with
+    separate video and text branches."""
+    rng = np.random.default_rng(23)
+    mlp, TXT = 128, 4
+    g = oracle.Geometry(1, 4, 6, (1, 30, 30), TXT, 1)
+    emb, _ = random_emb(rng, oracle)
+    vb = random_branch(rng, mlp)
+    tb = random_branch(rng, mlp)
+    tb2 = dict(tb)
+    tb2[key] = tb[key] + 0.5 + rng.standard_normal(tb[key].shape).astype(np.float32)
+    x = rng.standard_normal((g.Lv + TXT, 2560)).astype(np.float32)
+    for last in (True, False):
+        a = oracle.dit_layer(x[: g.Lv], x[g.Lv:], emb, vb, tb, g, txt_vid_only=last)
+        b = oracle.dit_layer(x[: g.Lv], x[g.Lv:], emb, vb, tb2, g, txt_vid_only=last)
+        if last:
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), key
+        else:
+            assert not np.array_equal(a[1], b[1]), key
+
+
+def test_last_layer_text_rows_closed_form(oracle):
+    """The text rows of the vid_only last layer are x_t + out_t(attention),
+    the attention's text input being the plain RMSNorm of x_t (no ada, no
+    gate, no MLP).  A full layer whose text branch modulates by the identity
+    (ada vectors that cancel emb's slots to scale 1, shift 0, gate 1) and
+    whose text MLP output weights are zero computes the same rows, up to the
+    last bits of the cancellations."""
+    rng = np.random.default_rng(24)
+    mlp, TXT = 128, 5
+    g = oracle.Geometry(1, 4, 6, (1, 30, 30), TXT, 0)
+    emb, _ = random_emb(rng, oracle)
+    vb = random_branch(rng, mlp)
+    tb = random_branch(rng, mlp)
+    # emb[6d + k] + vector = identity: scale 1 (k = 1), shift 0 (k = 0), gate 1 (k = 2)
+    ident = dict(tb)
+    ident["attn_shift"] = (-emb[0::6]).astype(np.float32)
+    ident["attn_scale"] = (1.0 - emb[1::6]).astype(np.float32)
+    ident["attn_gate"] = (1.0 - emb[2::6]).astype(np.float32)
+    ident["mlp_out_w"] = np.zeros_like(tb["mlp_out_w"])
+    x = rng.standard_normal((g.Lv + TXT, 2560)).astype(np.float32)
+    last = oracle.dit_layer(x[: g.Lv], x[g.Lv:], emb, vb, tb, g, txt_vid_only=True)
+    full = oracle.dit_layer(x[: g.Lv], x[g.Lv:], emb, vb, ident, g, txt_vid_only=False)
+    # the same arithmetic up to the multiplications by exactly 1 and additions of 0,
+    # which may differ in the last bit where emb's slots do not cancel exactly
+    cos, rel, _ = metrics(full[1] - x[g.Lv:], last[1] - x[g.Lv:])
+    assert cos >= 0.9999999 and rel <= 1e-5, (cos, rel)
+    cos, rel, _ = metrics(full[0], last[0])
+    assert cos >= 0.9999999 and rel <= 1e-5, (cos, rel)
+
+
 def test_patchify_known_answer():
     """Row (t, hh, ww), column (ph*2 + pw)*33 + c holds grid[t, 2hh+ph, 2ww+pw, c]
     (dit_vk.cpp:717-733), on a grid whose values encode their own indices."""

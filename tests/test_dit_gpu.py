@@ -93,16 +93,53 @@ def test_layer_small(oracle, ctx, kind, shifted):
         assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
 
 
-@pytest.mark.parametrize("kind", ["shared", "dual"])
-def test_layer_1080p(oracle, ctx, kind):
-    """One full-size layer (1x68x80 grid, TXT 58, MLP 6912), odd (shifted) geometry."""
-    note(f"layer 1080p {kind}")
-    x, out, ref, Lv = run_layer(oracle, ctx, (1, 68, 80), (4, 3, 3), 58, 1, 6912, kind, 50)
+@pytest.mark.parametrize("kind,mlp", [("shared", 6912), ("dual", 6912), ("shared", 10240)])
+def test_layer_1080p(oracle, ctx, kind, mlp):
+    """One full-size layer (1x68x80 grid, TXT 58), odd (shifted) geometry, at the
+    reference checkpoint's MLP width 6912 (dit_vk.cpp:19) and at the 10240 of
+    the DiT-step workload as BASELINE's config 3 writes it (timed by bench.py
+    as the MLP-10240 step)."""
+    note(f"layer 1080p {kind} mlp={mlp}")
+    x, out, ref, Lv = run_layer(oracle, ctx, (1, 68, 80), (4, 3, 3), 58, 1, mlp, kind, 50)
     for sl in (slice(0, Lv), slice(Lv, None)):
         cos, rel, _ = metrics(out[sl], ref[sl])
         dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
         note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
         assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
+
+
+@pytest.mark.parametrize("key", ["attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate"])
+def test_last_layer_ignores_text_ada(oracle, ctx, key):
+    """dit_layer_forward with txt_vid_only = 1 (forward_latent's last layer,
+    dit_vk.cpp:523-620): a different text-branch ada vector leaves every
+    output row unchanged, bit for bit; with txt_vid_only = 0 it changes the
+    text rows."""
+    import torch
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(70)
+    grid, nw, TXT, mlp = (1, 12, 20), (4, 3, 3), 9, 256
+    og = oracle.Geometry(*grid, nw, TXT, 1)
+    emb, _ = random_emb(rng, oracle)
+    vb = random_branch(rng, mlp, oracle)
+    tb = random_branch(rng, mlp, oracle)
+    tb2 = dict(tb)
+    tb2[key] = tb[key] + 0.5 + rng.standard_normal(tb[key].shape).astype(np.float32)
+    x = rng.standard_normal((og.Lv + TXT, 2560)).astype(np.float32)
+    geom = ctx.build_geometry(*grid, nw, TXT, 1)
+    dvb = to_device(vb, mlp, ctx, dev)
+    demb = torch.from_numpy(emb).to(dev)
+    for last in (True, False):
+        outs = []
+        for t in (tb, tb2):
+            dx = torch.from_numpy(x).to(dev)
+            ctx.layer(geom, dvb, to_device(t, mlp, ctx, dev), demb, dx, og.Lv, TXT, mlp=mlp, txt_vid_only=last)
+            torch.cuda.synchronize()
+            outs.append(dx.cpu().numpy())
+        if last:
+            assert np.array_equal(outs[0], outs[1]), key
+        else:
+            assert not np.array_equal(outs[0][og.Lv:], outs[1][og.Lv:]), key
+    geom.close()
 
 
 def test_embed_and_final(oracle, ctx):

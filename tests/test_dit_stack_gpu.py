@@ -3,9 +3,12 @@
 - 32-layer 1080p stack (1x68x80 latent tokens, 58 text rows, windows (4,3,3),
   MLP 6912; layers 0-9 with separate video/text branches, 10-31 shared; even
   layers unshifted, odd shifted; t = 1000; seed 3).  The hidden state after
-  layers 0, 1, 9, 10, 30 and 31 is compared with the layer reference fed the
-  GPU's own input to that layer (the reference compares after every layer,
-  dit_vk.cpp:638-654), at two levels:
+  every one of the 32 layers is compared with the layer reference fed the
+  GPU's own input to that layer, as the reference dumps and compares after
+  every layer (dit_vk.cpp:636-654); four tests of eight layers each (each
+  replays the device stack from layer 0 with the same seed), with the
+  reference's matrix products computed in fp32 on the device and its
+  attention by the oracle on the CPU.  Two levels:
     * the block's own rounding points (bf16 GEMM inputs, qkv, attention and
       SwiGLU outputs; weights as the bf16 values the device holds):
       cos >= 0.9999, update (x_out - x_in) cos >= 0.999;
@@ -88,10 +91,24 @@ def time_weights(gen):
     return [r(2560, 256), r(2560), r(2560, 2560), r(2560), r(15360, 2560), r(15360)]
 
 
-def check_layer(oracle, tag, x_in, out, emb, hosts, og, Lv, TXT):
+def device_mm():
+    """fp32 a @ w.T on the device (torch.mm, full fp32: no reduced-precision
+    inputs), for the layer reference at full size."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    def mm(a, w):
+        ta = torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+        tw = torch.from_numpy(np.ascontiguousarray(w, np.float32)).cuda()
+        return torch.mm(ta, tw.t().contiguous()).cpu().numpy()
+    return mm
+
+
+def check_layer(oracle, tag, x_in, out, emb, hosts, og, Lv, TXT, mm=None):
     (v16, t16), (vbf, tbf) = hosts
-    ref = layer_emulation(oracle, x_in, emb, vbf, tbf, og, Lv, TXT, bf16=True)
-    ref32 = layer_emulation(oracle, x_in, emb, v16, t16, og, Lv, TXT, bf16=False)
+    kw = {} if mm is None else {"mm": mm}
+    ref = layer_emulation(oracle, x_in, emb, vbf, tbf, og, Lv, TXT, bf16=True, **kw)
+    ref32 = layer_emulation(oracle, x_in, emb, v16, t16, og, Lv, TXT, bf16=False, **kw)
     for part, sl in (("vid", slice(0, Lv)), ("txt", slice(Lv, None))):
         cos, _, _ = metrics(out[sl], ref[sl])
         dcos, _, _ = metrics(out[sl] - x_in[sl], ref[sl] - x_in[sl])
@@ -103,19 +120,21 @@ def check_layer(oracle, tag, x_in, out, emb, hosts, og, Lv, TXT):
         assert cos32 >= BF16_COS, (tag, part, cos32)
 
 
-def test_cfg3_1080p_32_layers_layer_by_layer(oracle, ctx):
+@pytest.mark.parametrize("chunk", [0, 1, 2, 3])
+def test_cfg3_1080p_32_layers_layer_by_layer(oracle, ctx, chunk):
     import torch
     grid, nw, TXT, mlp = (1, 68, 80), (4, 3, 3), 58, 6912
-    keep = (0, 1, 9, 10, 30, 31)
+    keep = tuple(range(8 * chunk, 8 * chunk + 8))
+    mm = device_mm()
     gen = torch.Generator(device="cuda").manual_seed(3)
-    note("cfg3: 32 layers (10 dual + 22 shared), branches generated on the device")
+    note(f"cfg3: 32 layers (10 dual + 22 shared), branches generated on the device; layers {keep[0]}-{keep[-1]}")
     emb = ctx.time_embedding(1000.0, *time_weights(gen))
     Lv = grid[0] * grid[1] * grid[2]
     x = torch.randn((Lv + TXT, 2560), generator=gen, device="cuda")
     geoms = [ctx.build_geometry(*grid, nw, TXT, s) for s in (0, 1)]
     ogeoms = [oracle.Geometry(*grid, nw, TXT, s) for s in (0, 1)]
     emb_h = emb.cpu().numpy()
-    for i, vb, tb, hosts in stack_layers(ctx, gen, 32, 10, mlp, keep):
+    for i, vb, tb, hosts in stack_layers(ctx, gen, keep[-1] + 1, 10, mlp, keep):
         if i in keep:
             torch.cuda.synchronize()
             x_in = x.cpu().numpy()
@@ -123,7 +142,7 @@ def test_cfg3_1080p_32_layers_layer_by_layer(oracle, ctx):
         if i in keep:
             torch.cuda.synchronize()
             note(f"cfg3 layer {i} ({'dual' if i < 10 else 'shared'}, {'shifted' if i % 2 else 'unshifted'})")
-            check_layer(oracle, f"layer {i}", x_in, x.cpu().numpy(), emb_h, hosts, ogeoms[i % 2], Lv, TXT)
+            check_layer(oracle, f"layer {i}", x_in, x.cpu().numpy(), emb_h, hosts, ogeoms[i % 2], Lv, TXT, mm)
     assert bool(torch.isfinite(x).all())
     for g in geoms:
         g.close()

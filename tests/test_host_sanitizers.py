@@ -197,6 +197,23 @@ def test_graph(driver, tmp_path):
         q.write_text("\n".join(lines).replace(old, new) + "\n")
         rc, out = run(driver, "graph", q, binf, -1, "vid_out_norm_w")
         assert rc == -1
+    # value counts near 2^62 (tagged_bytes' 2 n + 3 and 4 n would overflow,
+    # a vector of that size would throw): refused before any arithmetic
+    text = "\n".join(lines)
+    for k, key in enumerate(("2=", "0=")):
+        ip = next(ln for ln in lines if ln.startswith("InnerProduct"))
+        tok = next(t for t in ip.split() if t.startswith(key))
+        for huge in ("4611686018427387904", "2305843009213693952", "9223372036854775807"):
+            q = tmp_path / f"huge_{k}_{huge[:4]}.param"
+            q.write_text(text.replace(ip, ip.replace(" " + tok, f" {key}{huge}"), 1) + "\n")
+            rc, out = run(driver, "graph", q, binf, -1, "vid_out_norm_w")
+            assert rc == -1, (key, huge)
+    rn = next(ln for ln in lines if ln.startswith("RMSNorm") and " 2=1" in ln)
+    tok = next(t for t in rn.split() if t.startswith("0="))
+    q = tmp_path / "huge_rms.param"
+    q.write_text(text.replace(rn, rn.replace(" " + tok, " 0=4611686018427387904"), 1) + "\n")
+    rc, out = run(driver, "graph", q, binf, -1, "vid_out_norm_w")
+    assert rc == -1
     for drop in (1, 2, 5, len(lines) // 2, len(lines) - 1):
         q = tmp_path / f"md_{drop}.param"
         q.write_text("\n".join(lines[:drop] + lines[drop + 1:]) + "\n")

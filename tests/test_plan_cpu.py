@@ -3,9 +3,12 @@ seedvr2-2b-ncnn_amd/csrc/awa_capi.cpp) on the CPU, through the driver
 tests/cpp/test_plan.cpp (built with hipcc, linked against the built library;
 no device call):
 every (head, work item) of a geometry scheduled exactly once with matching
-descriptors, the items of one (window, head) on one XCD, and the makespan no
-worse than plain longest-first; on the 1080p unshifted layer, where first fit
-decreasing packs the few item sizes better, strictly lower.
+descriptors, the items of one (window, head) on one XCD, the makespan no
+worse than plain longest-first (on the 1080p unshifted layer, where first fit
+decreasing packs the few item sizes better, strictly lower), and the kernel's
+DMA stream replayed slot by slot: every key tile an item reads is the one its
+fetch two (K) or one (V) tiles earlier put into the ring, including items of
+a window without video rows (one text tile of its own, padded to two).
 """
 import os
 import re
@@ -35,9 +38,10 @@ def driver(tmp_path_factory):
     return exe
 
 
-def run(driver, t, h, w, nw, txt, shifted, slots):
-    r = subprocess.run([driver] + [str(x) for x in (t, h, w, *nw, txt, shifted, slots)], capture_output=True,
-                       text=True, timeout=120)
+def run(driver, t, h, w, nw, txt, shifted, slots, empty_at=None):
+    extra = [] if empty_at is None else [empty_at]
+    r = subprocess.run([driver] + [str(x) for x in (t, h, w, *nw, txt, shifted, slots, *extra)],
+                       capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("rc=0"), r.stdout[-2000:] + r.stderr[-2000:]
     m = re.search(r"makespan (\d+) lpt (\d+) mean ([\d.]+)", r.stdout)
     return int(m.group(1)), int(m.group(2)), float(m.group(3))
@@ -66,3 +70,13 @@ def test_schedule_covers_every_item(driver, case):
 def test_packing_beats_longest_first_on_1080p(driver):
     mk, lpt, mean = run(driver, 1, 68, 80, (4, 3, 3), 58, 0, 512)
     assert mk < lpt, (mk, lpt)
+
+
+@pytest.mark.parametrize("txt", [1, 58, 64, 65])
+@pytest.mark.parametrize("empty_at", [0, 3, 9])
+def test_stream_with_empty_window(driver, txt, empty_at):
+    """An injected geometry may hold a window without video rows (awa_geom_set
+    with a repeated cumf entry, a win file with an empty slice); with at most
+    64 text rows its work item has one key tile of its own."""
+    mk, lpt, mean = run(driver, 1, 23, 27, (4, 3, 3), txt, 0, 16, empty_at)
+    assert mk <= lpt and mk >= mean
