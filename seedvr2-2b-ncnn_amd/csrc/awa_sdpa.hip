@@ -93,9 +93,18 @@ __device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, vo
 //   A(u)  MFMA  S(u+1) = K(u+1) Q^T - m         (2 x 9 MFMAs: a bias k-step
 //                                               adds -m, m a bf16 value)
 //         VALU  P(u) = exp2(S(u))               (32 exponentials)
+//         LDS   V^T(u) fragments                (16 transposed reads)
 //   B(u)  MFMA  O^T += V^T(u) P^T(u)            (16 MFMAs)
 //         VALU  row maximum of S(u+1), row sums of P(u)
+//         LDS   K(u+2) fragments                (8 reads, one per MFMA)
 //
+// With one wave per SIMD the LDS answers a wave's reads with a latency of a
+// few hundred cycles (its read rate grows with the reads in flight: about
+// 90 B/clk/CU from four waves, 170-190 from sixteen, measured), so each
+// fragment is read a phase before its MFMAs: the K fragments of unit u + 2
+// during phase B of unit u, from asm (the compiler does not track them; the
+// next phase A starts with an explicit wait naming their registers), and the
+// V^T fragments early in phase A, pinned there by a scheduling group.
 // Phase A is written with the compiler's MFMA and exp2 builtins, ordered two
 // exponentials then one MFMA by sched_group_barrier, and the scores live in
 // two register sets that alternate between units (unit u exponentiates set
@@ -247,6 +256,12 @@ __device__ inline void sum_pv(f32x16& o, const bf16x8& v, const bf16x8& p, float
         "v_mfma_f32_32x32x16_bf16 %0, %2, %3, %0"
         : "+a"(o), "+v"(ps)
         : "v"(v), "v"(p), "v"(x0), "v"(x1));
+}
+// K fragment read issued from asm (the compiler neither counts it nor waits
+// for it; the next phase A's start waits for it explicitly, naming the
+// registers).
+__device__ inline void ds_read_kf(bf16x8& d, uint32_t addr) {
+    asm volatile("ds_read_b128 %0, %1" : "=a"(d) : "v"(addr));
 }
 // bf16 value nearest to x (round to nearest even), as a float.
 __device__ inline float bf16_round(float x) { return __uint_as_float(bf16_rne(x) << 16); }
@@ -564,14 +579,18 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                      : "memory");
         __syncthreads();
 
+        // K fragments of the next unit's score MFMAs, read a phase ahead
+        bf16x8 kfn[8];
         // Unit 0: raw scores, m = their row maximum (rounded to bf16), scores
         // relative to m.
         if (active) {
             f32x16 s0[2];
             bf16x8 kf[8];
-            const int ko = k_ofs(0);
+            const int ko = k_ofs(0), ko1 = k_ofs(1);
 #pragma unroll
             for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
+#pragma unroll
+            for (int st = 0; st < 8; st++) ds_read_kf(kfn[st], lds_base + 2 * (ko1 + kadr[st]));
 #pragma unroll
             for (int st = 0; st < 8; st++)
 #pragma unroll
@@ -601,7 +620,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
         // offsets): a 1 KiB instruction occupies the CU's address unit for 16
         // cycles, so issued back to back they would stall the wave, while one
         // per 32-cycle MFMA goes through without a stall.
-        auto unit = [&](int u, bool has_succ, bool dma) __attribute__((always_inline)) {
+        auto unit = [&](int u, bool has_succ, bool dma, bool pf) __attribute__((always_inline)) {
             // ---- stale-maximum rule for this unit's scores (mtc: their row max relative to m)
             if (__any(mtc[0] > RESCALE_LOG2 || mtc[1] > RESCALE_LOG2)) {
                 float alpha[2];
@@ -648,13 +667,14 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             float ps[2] = {0.f, 0.f};
             if (has_succ) {
                 // ---- phase A: S(u+1) MFMAs with the exponentials of this unit
-                bf16x8 kf[8];
-                const int ko = k_ofs(u + 1);
                 const bf16x8 onesm = mask_frag(unit_kv(u + 1), n, hb);
                 if (dma) m0_set(dk_m);
-#pragma unroll
-                for (int st = 0; st < 8; st++) kf[st] = *reinterpret_cast<const bf16x8*>(lds + ko + kadr[st]);
-                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the eight K fragment reads first
+                bf16x8 (&kf)[8] = kfn;  // read in the previous phase B (or at the item start)
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+a"(kfn[0]), "+a"(kfn[1]), "+a"(kfn[2]), "+a"(kfn[3]), "+a"(kfn[4]),
+                               "+a"(kfn[5]), "+a"(kfn[6]), "+a"(kfn[7])
+                             :
+                             : "memory");
                 // 18 slots: slot 0 / 1 are the bias k-steps of blocks 0 / 1, slot
                 // j >= 2 k-step (j - 2) / 2 of block j & 1; exponentials two per
                 // slot, block 0 in slots 0-7, block 1 in slots 8-15.
@@ -672,7 +692,10 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                         snx[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[qb][st], snx[qb], 0, 0, 0);
                     if (j < 16) __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (j == 3) load_vf();
+                    if (j == 3) {
+                        load_vf();
+                        __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the V^T reads here
+                    }
                     if (dma && j >= 2 && j < 10) dma_k_i(j - 2);
                     if (dma && j >= 10) dma_v_i(j - 10);
                     if (dma && j == 17) load_vt(nv_tile);
@@ -697,6 +720,12 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 for (int c2 = 0; c2 < 2; c2++)
 #pragma unroll
                     for (int i = 0; i < 8; i++) pb[qb][c2][i] = (__bf16)p[qb][8 * c2 + i];
+            // the K fragments of unit u + 2 (the next phase A): one read after
+            // each of phase B's first eight MFMAs
+            const uint32_t kpf = lds_base + 2 * k_ofs(u + 2);
+            auto prefetch_k = [&](int j) __attribute__((always_inline)) {
+                if (pf && j < 8) ds_read_kf(kfn[j], kpf + 2 * kadr[j]);
+            };
             if (has_succ) {
                 // ---- phase B: P.V MFMAs with the row maxima of S(u+1) and the row sums of P(u)
                 float mx[2] = {-INFINITY, -INFINITY};
@@ -706,6 +735,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     const int eq = j >> 3, er = 2 * (j & 7);                // max / sum items
                     max_sum_pv(oacc[qb][dt], vf[c2][dt], pb[qb][c2], mx[eq], snx[eq][er], snx[eq][er + 1],
                                ps[eq], p[eq][er], p[eq][er + 1]);
+                    prefetch_k(j);
                 }
                 mtc[0] = max_pair(mx[0]);
                 mtc[1] = max_pair(mx[1]);
@@ -716,6 +746,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     const int qb = j & 1, dt = (j >> 1) & 3, c2 = j >> 3;
                     const int eq = j >> 3, er = 2 * (j & 7);
                     sum_pv(oacc[qb][dt], vf[c2][dt], pb[qb][c2], ps[eq], p[eq][er], p[eq][er + 1]);
+                    prefetch_k(j);
                 }
             }
             l_i[0] += ps[0];
@@ -755,7 +786,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             set_v(vh, vtxt, (vb + kk + 1) & 1, !v_nxt || has_next);
             prep_v();
             if (active) {
-                unit(2 * kk, true, true);
+                unit(2 * kk, true, true, !last);
             } else {  // an idle wave still fills its half of the tiles
                 dma_k_all();
                 dma_v_all();
@@ -765,7 +796,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
             // next item's query tile loads during it (after the slot's last
             // item: the same tile again, unused)
             if (last) load_q(nxt);
-            if (active) unit(2 * kk + 1, !last, false);
+            if (active) unit(2 * kk + 1, !last, false, !last);
             if (!last) {
                 wait_vmem();
                 __syncthreads();
@@ -815,9 +846,14 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     ofs[i] = tok >= 0 ? (uint32_t)tok * (2 * DIM) + col : 0x80000000u;
                 }
                 uint16_t* stg = lds + (wave == 0 ? (kb + nk - 1) % 3 : 3 + ((vb + nk - 1) & 1)) * KT_E;
+                // the lane's swizzle terms, formed here (an opaque copy keeps
+                // the compiler from computing the twenty staging addresses
+                // once and holding them in registers across the item loop)
+                int nn = n, ln = lane;
+                asm volatile("" : "+v"(nn), "+v"(ln));
 #pragma unroll
                 for (int qb = 0; qb < 2; qb++) {
-                    const int row = 32 * qb + n;
+                    const int row = 32 * qb + nn;
 #pragma unroll
                     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -834,7 +870,7 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                 u32x4 v[16];
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const int row = 4 * i + (lane >> 4), c = lane & 15;
+                    const int row = 4 * i + (ln >> 4), c = ln & 15;
                     v[i] = *reinterpret_cast<const u32x4*>(stg + row * HEAD_D + ((c ^ (row & 15)) << 3));
                 }
 #pragma unroll

@@ -1,16 +1,19 @@
-"""Static check of the attention kernel's hand-placed query-fragment loads.
+"""Static check of the attention kernel's hand-placed fragment loads.
 
 sdpa_bf16_kernel (seedvr2-2b-ncnn_amd/csrc/awa_sdpa.hip) loads the next work
 item's query fragments with inline-asm `global_load_dwordx4 a[..]` straight
 into accumulation registers while the current item finishes, and waits for
-them with the item start's `s_waitcnt vmcnt(0)`.  The compiler does not see
-those loads as loads: if it ever placed a copy or any other use of those
-registers between a load and that wait (a phi copy on a loop edge, a move
-under register pressure), the use would read stale data without any error.
-This test compiles the kernel to AMD assembly with the library's own flags
-(Makefile) and proves on its control-flow graph that on every path from such a
-load no instruction touches the loaded registers before an `s_waitcnt
-vmcnt(0)`.  The analysis is checked on planted mistakes first.  A second
+them with the item start's `s_waitcnt vmcnt(0)`; it reads the next
+unit's K fragments with inline-asm `ds_read_b128 a[..]` a phase early and
+waits for them with `s_waitcnt lgkmcnt(0)`.  The compiler does not see those
+loads as loads: if it ever placed a copy or any other use of those registers
+between a load and its wait (a phi copy on a loop edge, a move under register
+pressure), the use would read stale data without any error.  This test
+compiles the kernel to AMD assembly with the library's own flags (Makefile)
+and proves on its control-flow graph that on every path from such a load no
+instruction touches the loaded registers before a wait that covers it
+(`vmcnt(0)` for vector memory loads, `lgkmcnt(0)` for LDS reads).  The
+analysis is checked on planted mistakes first.  A second
 check: the kernel's LDS DMA takes its destination from M0, written by the
 kernel's asm once per four DMA instructions, so no compiler-generated
 instruction may write M0 anywhere in the kernel.
@@ -30,6 +33,7 @@ HIPCC = "/opt/rocm/bin/hipcc"
 AREG = re.compile(r"\ba\[(\d+):(\d+)\]|\ba(\d+)\b")
 LABEL = re.compile(r"^(\.LBB\d+_\d+):")
 VMEM_LOAD = re.compile(r"^(global|buffer|flat)_load_")
+LDS_LOAD = re.compile(r"^ds_read")
 
 
 def makefile_flags():
@@ -71,10 +75,11 @@ def parse(asm_text):
     return out
 
 
-def check(insts):
+def check(insts, load=VMEM_LOAD, wait=r"vmcnt\(0\)"):
     """Returns the violations: (block, instruction, registers) where a
-    register loaded by an AGPR-destination vector load is touched before an
-    s_waitcnt vmcnt(0) on some path, and the number of such loads."""
+    register loaded by an AGPR-destination load (vector memory, or with
+    load=LDS_LOAD an LDS read) is touched before an s_waitcnt covering it
+    (wait) on some path, and the number of such loads."""
     # basic blocks
     blocks, order = {}, []
     cur = "entry"
@@ -109,18 +114,18 @@ def check(insts):
             if nxt is not None:
                 s.append(nxt)
         succ[b] = [x for x in s if x in blocks]
-    n_loads = sum(1 for b in order for op, rest in blocks[b] if VMEM_LOAD.match(op) and rest.startswith("a"))
+    n_loads = sum(1 for b in order for op, rest in blocks[b] if load.match(op) and rest.startswith("a"))
     pend_in = {b: set() for b in order}
     violations = []
 
     def run(b, pending, record):
         pending = set(pending)
         for op, rest in blocks[b]:
-            if op == "s_waitcnt" and re.search(r"vmcnt\(0\)", rest):
+            if op == "s_waitcnt" and re.search(wait, rest):
                 pending.clear()
                 continue
             r = regs(rest)
-            if VMEM_LOAD.match(op) and rest.startswith("a"):
+            if load.match(op) and rest.startswith("a"):
                 pending |= r
                 continue
             hit = r & pending
@@ -181,6 +186,19 @@ def test_query_fragment_loads_are_waited_for(sdpa_asm):
     violations, n_loads = check(parse(sdpa_asm))
     assert n_loads >= 16, "no asm query-fragment loads found: the check would be vacuous"
     assert not violations, violations[:5]
+
+
+def test_k_fragment_reads_are_waited_for(sdpa_asm):
+    insts = parse(sdpa_asm)
+    violations, n_loads = check(insts, LDS_LOAD, r"lgkmcnt\(0\)")
+    assert n_loads >= 16, "no asm K-fragment reads found: the check would be vacuous"
+    assert not violations, violations[:5]
+    # a planted use right after such a read is found
+    k = next(i for i, (lab, op, rest) in enumerate(insts) if op and LDS_LOAD.match(op) and rest.startswith("a"))
+    reg = min(regs(insts[k][2]))
+    planted = insts[:k + 1] + [(None, "v_accvgpr_read_b32", f"v0, a{reg}")] + insts[k + 1:]
+    v, _ = check(planted, LDS_LOAD, r"lgkmcnt\(0\)")
+    assert any(reg in hit for _, _, hit in v)
 
 
 M0_WRITE = re.compile(r"^\s*s_\w+\s+m0\b")
