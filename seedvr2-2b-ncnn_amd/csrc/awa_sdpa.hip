@@ -293,6 +293,20 @@ __device__ inline bf16x8 mask_frag(int kv, int n, int hb) {
 __device__ inline void mfma_fence_v(f32x16 (&s)[2]) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(s[0]), "+v"(s[1]));
 }
+// The compiler places no wait states before an asm statement for what the
+// instructions before it wrote, so the asm of phase B, which reads the results
+// of the score MFMAs (builtins: a VALU read needs twelve wait states after
+// v_mfma_f32_32x32x16_bf16) and of the exponentials (v_exp_f32: one), comes
+// after this fence: it ties both register sets and waits sixteen.  Without it
+// the scheduler may end phase A with the MFMA whose scores phase B's first
+// maximum reads, which then sees the registers' previous contents.
+__device__ inline void score_fence(f32x16 (&s)[2], f32x16 (&p)[2]) {
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(s[0]), "+v"(s[1]), "+v"(p[0]), "+v"(p[1]));
+}
+// The same after the exponentials of an item's last unit (no MFMA results).
+__device__ inline void exp_fence(f32x16 (&p)[2]) {
+    asm volatile("s_nop 1" : "+v"(p[0]), "+v"(p[1]));
+}
 __device__ inline void acc_fence(f32x16 (&o)[2][4]) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                  : "+a"(o[0][0]), "+a"(o[0][1]), "+a"(o[0][2]), "+a"(o[0][3]),
@@ -704,12 +718,14 @@ void sdpa_bf16_kernel(SdpaArgs a) {
                     // burst; a full scheduling barrier keeps each at its slot
                     if (dma && j >= 2) __builtin_amdgcn_sched_barrier(0);
                 }
+                score_fence(snx, p);
             } else {
                 load_vf();
 #pragma unroll
                 for (int qb = 0; qb < 2; qb++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) p[qb][r] = __builtin_amdgcn_exp2f(p[qb][r]);
+                exp_fence(p);
             }
             // P^T in the B-operand order of O^T += V^T P^T: element i of
             // pb[qb][c2] is register 8 c2 + i of S^T[qb]

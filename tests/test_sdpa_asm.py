@@ -16,7 +16,10 @@ instruction touches the loaded registers before a wait that covers it
 analysis is checked on planted mistakes first.  A second
 check: the kernel's LDS DMA takes its destination from M0, written by the
 kernel's asm once per four DMA instructions, so no compiler-generated
-instruction may write M0 anywhere in the kernel.
+instruction may write M0 anywhere in the kernel.  A third: the compiler puts
+no wait states before an inline-asm statement, so asm that reads MFMA (or
+transcendental) results must be fenced by the kernel itself; every such read
+in the library's MFMA kernels is checked for its wait states on every path.
 """
 import os
 import re
@@ -238,3 +241,164 @@ def test_m0_written_only_by_the_kernels_asm(sdpa_asm):
     planted = sdpa_asm.replace(";;#ASMSTART", "\ts_mov_b32 m0, -1\n\t;;#ASMSTART", 1)
     _, outside2 = m0_writes(planted)
     assert outside2 == ["s_mov_b32 m0, -1"]
+
+
+# Wait states a read needs after the write of its register (gfx950), as the
+# compiler inserts them for its own instructions: a VALU, memory or MFMA
+# source read of a v_mfma_f32_32x32x16_bf16 result 12 (s_nop 11), of a
+# v_mfma_f32_16x16x32_bf16 result 8, of a v_mfma_f32_32x32x2_f32 result 18;
+# a read of a transcendental result one.
+MFMA_READ_WAIT = {"v_mfma_f32_32x32x16_bf16": 12, "v_mfma_f32_16x16x32_bf16": 8, "v_mfma_f32_32x32x2_f32": 18}
+TRANS_READ_WAIT = 1
+VREG = re.compile(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b")
+TRANS = re.compile(r"^v_(exp|log|rcp|rsq|sqrt|sin|cos)_f32")
+
+
+def vregs(operands):
+    out = set()
+    for m in VREG.finditer(operands):
+        if m.group(1):
+            out.update((m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1))
+        else:
+            out.add((m.group(4), int(m.group(5))))
+    return out
+
+
+def wait_state_violations(insts):
+    """Reads of MFMA or transcendental results with fewer wait states between
+    write and read than the hardware needs, on any control-flow path.  The
+    compiler inserts these waits for its own instructions but not before an
+    inline-asm statement, so asm that reads such results must be preceded by an
+    explicit fence.  An MFMA's accumulator operand (src2) is exempt: a chain of
+    MFMAs on one accumulator is interlocked."""
+    blocks, order, cur, anon = {"entry": []}, ["entry"], "entry", 0
+    for lab, op, rest in insts:
+        if lab is not None:
+            cur = lab
+            blocks[cur] = []
+            order.append(cur)
+            continue
+        blocks[cur].append((op, rest))
+        if op.startswith("s_branch") or op.startswith("s_cbranch") or op == "s_endpgm":
+            anon += 1
+            cur = f"anon{anon}"
+            blocks[cur] = []
+            order.append(cur)
+    succ = {}
+    for i, b in enumerate(order):
+        body, nxt = blocks[b], (order[i + 1] if i + 1 < len(order) else None)
+        last = body[-1] if body else None
+        s = []
+        if last and last[0] == "s_endpgm":
+            pass
+        elif last and last[0].startswith("s_branch"):
+            s.append(last[1].split()[0])
+        else:
+            if last and last[0].startswith("s_cbranch"):
+                s.append(last[1].split()[0])
+            if nxt is not None:
+                s.append(nxt)
+        succ[b] = [x for x in s if x in blocks]
+
+    def step(b, state, record, out):
+        state = dict(state)
+        for op, rest in blocks[b]:
+            ops = [o.strip() for o in rest.split(",")] if rest else []
+            if op.startswith("v_") or op.startswith("ds_") or op.startswith("buffer_") or op.startswith("global_"):
+                if op.startswith("v_mfma"):
+                    srcs = ops[1:3]
+                elif op.startswith("ds_write") or op.startswith("buffer_store") or op.startswith("global_store"):
+                    srcs = ops
+                elif op.startswith("v_"):
+                    srcs = ops[1:]
+                else:
+                    srcs = ops[1:]
+                rd = set()
+                for o in srcs:
+                    rd |= vregs(o)
+                hit = {r for r in rd if state.get(r, 0) > 0}
+                if hit and record:
+                    out.append((b, f"{op} {rest}", sorted(hit)[:4]))
+            n = 1
+            if op == "s_nop":
+                n = int(rest.split()[0], 0) + 1
+            state = {r: w - n for r, w in state.items() if w - n > 0}
+            if op.startswith("v_mfma") and ops:
+                for r in vregs(ops[0]):
+                    state[r] = MFMA_READ_WAIT.get(op, 18)
+            elif TRANS.match(op) and ops:
+                for r in vregs(ops[0]):
+                    state[r] = max(state.get(r, 0), TRANS_READ_WAIT)
+        return state
+
+    st_in = {b: {} for b in order}
+    changed = True
+    while changed:
+        changed = False
+        for b in order:
+            o = step(b, st_in[b], False, None)
+            for s in succ[b]:
+                m = dict(st_in[s])
+                for r, w in o.items():
+                    if w > m.get(r, 0):
+                        m[r] = w
+                if m != st_in[s]:
+                    st_in[s] = m
+                    changed = True
+    out = []
+    for b in order:
+        step(b, st_in[b], True, out)
+    return out
+
+
+def test_mfma_results_read_after_enough_wait_states(sdpa_asm):
+    """Phase B's asm reads the score MFMAs' results (row maxima) and the
+    exponentials (row sums); the compiler puts no wait states before asm, so
+    the kernel fences them itself.  Every read of an MFMA or transcendental
+    result in the kernel, compiler-generated or asm, must have its wait
+    states on every path."""
+    insts = parse(sdpa_asm)
+    assert sum(1 for _, op, _ in insts if op and op.startswith("v_mfma")) >= 64
+    v = wait_state_violations(insts)
+    assert not v, v[:5]
+    # a planted asm-style read right after an MFMA is found, and one behind
+    # s_nop 11 is not
+    k = next(i for i, (lab, op, rest) in enumerate(insts) if op and op.startswith("v_mfma") and rest.startswith("v["))
+    dst = insts[k][2].split(",")[0].strip()
+    first = dst[2:].split(":")[0]
+    planted = insts[:k + 1] + [(None, "v_max3_f32", f"v255, v255, v{first}, v{first}")] + insts[k + 1:]
+    assert any(("v", int(first)) in hit for _, _, hit in wait_state_violations(planted))
+    fenced = insts[:k + 1] + [(None, "s_nop", "11"), (None, "v_max3_f32", f"v255, v255, v{first}, v{first}")] + \
+        insts[k + 1:]
+    assert not any("v255, v255" in ins for _, ins, _ in wait_state_violations(fenced))
+
+
+@pytest.mark.parametrize("src", ["awa_sdpa_f32", "dit_gemm"])
+def test_other_mfma_kernels_wait_states(tmp_path, src):
+    """The same wait-state check over the library's other MFMA kernels (the
+    fp32 attention kernel and every GEMM instantiation), whose epilogues read
+    accumulators after asm fences."""
+    if not os.path.exists(HIPCC):
+        pytest.skip("hipcc not present")
+    r = subprocess.run(["make", "-n", "-B", "-C", PKG, f"_build/{src}.o"], capture_output=True, text=True, timeout=60)
+    line = next(l for l in r.stdout.split("\n") if f"{src}.hip" in l and "hipcc" in l)
+    flags = [t for t in shlex.split(line.split(" -c ")[0])[1:] if t != "-fPIC"]
+    out = tmp_path / f"{src}.s"
+    r = subprocess.run([HIPCC] + flags + ["--cuda-device-only", "-S", os.path.join(PKG, "csrc", f"{src}.hip"), "-o",
+                                          str(out)], cwd=PKG, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    text = open(out).read()
+    kernels = re.findall(r"^(_Z\S+):", text, re.M)
+    assert kernels
+    global KERNEL
+    saved, n_mfma = KERNEL, 0
+    try:
+        for k in kernels:
+            KERNEL = k
+            insts = parse(text)
+            n_mfma += sum(1 for _, op, _ in insts if op and op.startswith("v_mfma"))
+            v = wait_state_violations(insts)
+            assert not v, (k, v[:5])
+    finally:
+        KERNEL = saved
+    assert n_mfma >= 64
