@@ -178,6 +178,13 @@ int awa_cast_f32_to_bf16(awa_ctx* ctx, const float* d_in, uint16_t* d_out, int64
 int awa_cast_bf16_to_f32(awa_ctx* ctx, const uint16_t* d_in, float* d_out, int64_t n,
                          awa_stream_t stream);
 
+/* Streaming device copy of `bytes` (a multiple of 16) from d_src to d_dst.
+ * No counterpart in the reference: it is the measuring stick for the
+ * HBM-bound passes (the fastest hand-written copy of those measured on the
+ * MI355X, timed beside them by bench.py and used to calibrate the HBM byte
+ * counters). */
+int awa_stream_copy(awa_ctx* ctx, void* d_dst, const void* d_src, int64_t bytes, awa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

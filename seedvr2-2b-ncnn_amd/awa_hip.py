@@ -143,6 +143,7 @@ def lib():
                                        vp, vp]
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
+        L.awa_stream_copy.argtypes = [vp, vp, vp, C.c_int64, vp]
         _lib = L
     return _lib
 
@@ -377,6 +378,16 @@ class Context:
         rc = lib().awa_cast_bf16_to_f32(self.ptr, C.c_void_p(src.data_ptr()), C.c_void_p(out.data_ptr()),
                                         src.numel(), _stream_ptr(stream))
         self.check(rc, "awa_cast_bf16_to_f32")
+        return out
+
+    def stream_copy(self, src, out, stream=None):
+        """awa_stream_copy: device copy of src's bytes into out (the HBM ceiling's copy kernel)."""
+        nb = src.numel() * src.element_size()
+        if out.numel() * out.element_size() != nb or not (src.is_contiguous() and out.is_contiguous()):
+            raise ValueError("stream_copy: contiguous source and output of one byte size")
+        rc = lib().awa_stream_copy(self.ptr, C.c_void_p(out.data_ptr()), C.c_void_p(src.data_ptr()), nb,
+                                   _stream_ptr(stream))
+        self.check(rc, "awa_stream_copy")
         return out
 
     # ---- the DiT block (include/dit_capi.h)

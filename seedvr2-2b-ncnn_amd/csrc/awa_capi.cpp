@@ -949,4 +949,14 @@ int awa_cast_bf16_to_f32(awa_ctx* ctx, const uint16_t* d_in, float* d_out, int64
     return AWA_OK;
 }
 
+int awa_stream_copy(awa_ctx* ctx, void* d_dst, const void* d_src, int64_t bytes, awa_stream_t stream) {
+    if (!ctx || bytes < 0 || bytes % 16 != 0 || (bytes > 0 && (!d_dst || !d_src))) {
+        set_err(ctx, "awa_stream_copy: bad argument (bytes must be a multiple of 16)");
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    HIPCK(ctx, launch_stream_copy(d_dst, d_src, (size_t)bytes, reinterpret_cast<hipStream_t>(stream)));
+    return AWA_OK;
+}
+
 }  // extern "C"

@@ -298,5 +298,6 @@ hipError_t launch_coalesce(int dtype, const float* tpart, void* tattn, int nwin,
 hipError_t launch_cast_f32_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s);
 hipError_t launch_cast_bf16_f32(const uint16_t* in, float* out, int64_t n, hipStream_t s);
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 
 }  // namespace awa

@@ -1,8 +1,9 @@
 // awa_pack.hip — fused qk RMSNorm + 3-D RoPE + window partition.
 //
-// One workgroup per (64-row tile, head); the 20 heads of a tile are
-// neighbouring work indices on one XCD, so the tile's (cos, sin) rows come
-// from HBM once and from that XCD's L2 for the other heads.  It gathers the
+// One workgroup per (64-row tile, head) for fp32 storage, per (tile, two
+// heads) for bf16; the workgroups of a tile are neighbouring work indices on
+// one XCD, so the tile's (cos, sin) rows come from HBM once and from that
+// XCD's L2 for the other heads.  It gathers the
 // tile's rows from vqkv / tqkv (window order of vidx, awa_vk.cpp:73-88, through
 // the geometry's row table),
 // normalises q and k per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 +
@@ -223,14 +224,131 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     }
 }
 
+// bf16 storage: one workgroup per (64-row tile, group of PACK_HG heads).  A
+// thread's row offsets, (cos, sin) pairs and gains are the same for every head
+// of the tile, so the workgroup loads them once and keeps them in registers for
+// its heads (each thread needs only its own rows' pairs: no exchange through
+// LDS); the q and k loads of the next head are in flight while the current
+// head is normalised, rotated and stored.  The output is rounded to bf16, so
+// the arithmetic is the short form: 1/r by v_rsq_f32 (within an ulp of the
+// correctly rounded sqrt and division of the fp32 kernel) and
+// y = ((x g) c -/+ (x' g') s) (1/r [* qscale]), eight operations per channel
+// pair where the exact form takes fourteen.
+constexpr int PACK_HG = 2;  // heads per workgroup (measured against 1, 4, 5 and 10 at 360p-1080p)
+
+__global__ __launch_bounds__(256) void pack_bf16_kernel(PackArgs a) {
+    using IO = Io<uint16_t>;
+    constexpr int NG = HEADS / PACK_HG;
+    static_assert(HEADS % PACK_HG == 0, "head groups must tile the heads");
+    const int nblk = a.n_tiles * NG;
+    const int lid = xcd_remap(nblk);  // a tile's groups: neighbouring ids, one XCD
+    if (lid >= nblk) return;
+    const int tile = lid / NG;
+    const int h0 = (lid - tile * NG) * PACK_HG;
+    const int tid = threadIdx.x;
+    const int c = tid & 15;
+    const int r0 = tid >> 4;
+
+    const bool is_txt = tile >= a.n_vid_tiles;
+    const int2 meta = reinterpret_cast<const int2*>(a.tile_meta)[tile];
+    const uint32_t* rows =
+        a.vrow + (size_t)(is_txt ? a.n_vid_tiles + (tile - a.n_vid_tiles) % a.ntt : tile) * TILE;
+    uint32_t ridx[RPT];
+#pragma unroll
+    for (int kk = 0; kk < RPT; kk++) ridx[kk] = rows[vrow_pos(r0 + 16 * kk)];
+    const int nvalid = meta.y;
+    const size_t cs_row0 = (size_t)meta.x;
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(is_txt ? a.tqkv : a.vqkv);
+    const float4* cst = reinterpret_cast<const float4*>(is_txt ? a.tcs : a.vcs);
+    const float* gq = is_txt ? a.nq_t : a.nq_v;
+    const float* gk = is_txt ? a.nk_t : a.nk_v;
+
+    // q and k of head h for the thread's rows (zeros for padding rows)
+    auto load_head = [&](int h, IO::Raw (&q)[RPT], IO::Raw (&k)[RPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < RPT; kk++) {
+            if (r0 + 16 * kk < nvalid) {  // uniform across the 16 lanes of a row
+                const uint16_t* row = src + (size_t)ridx[kk] + h * HEAD_D + c * 8;
+                q[kk] = IO::load(row);
+                k[kk] = IO::load(row + DIM);
+            } else {
+                q[kk] = k[kk] = IO::zero();
+            }
+        }
+    };
+    IO::Raw rq[2][RPT], rk[2][RPT];
+    load_head(h0, rq[0], rk[0]);
+    float4 cs[RPT][2];
+#pragma unroll
+    for (int kk = 0; kk < RPT; kk++) {
+        const int r = r0 + 16 * kk;
+        if (r < nvalid) {
+            const float4* p = cst + ((cs_row0 + r) * CS_STRIDE + c * 4) / 2;
+            cs[kk][0] = p[0];
+            cs[kk][1] = p[1];
+        } else {
+            cs[kk][0] = cs[kk][1] = make_float4(1.f, 0.f, 1.f, 0.f);
+        }
+    }
+    float gqv[8], gkv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        gqv[i] = gq[c * 8 + i];
+        gkv[i] = gk[c * 8 + i];
+    }
+    // y (8 channels of one row, normalised, gained and rotated, times s)
+    auto rope8 = [&](float (&x)[8], const float (&g)[8], float s, const float (&csv)[8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float cn = csv[2 * p], sn = csv[2 * p + 1];
+            const float p0 = x[2 * p] * g[2 * p], p1 = x[2 * p + 1] * g[2 * p + 1];
+            x[2 * p] = __builtin_fmaf(p0, cn, -(p1 * sn)) * s;
+            x[2 * p + 1] = __builtin_fmaf(p1, cn, p0 * sn) * s;
+        }
+    };
+
+#pragma unroll
+    for (int j = 0; j < PACK_HG; j++) {
+        const int h = h0 + j;
+        if (j + 1 < PACK_HG) load_head(h + 1, rq[(j + 1) & 1], rk[(j + 1) & 1]);
+        const size_t tile_off = ((size_t)h * a.n_tiles + tile) * TILE * HEAD_D;
+        uint16_t* Qt = reinterpret_cast<uint16_t*>(a.Qp) + tile_off;
+        uint16_t* Kt = reinterpret_cast<uint16_t*>(a.Kp) + tile_off;
+#pragma unroll
+        for (int kk = 0; kk < RPT; kk++) {
+            const int r = r0 + 16 * kk;
+            float q[8], k[8];
+            IO::widen(rq[j & 1][kk], q);
+            IO::widen(rk[j & 1][kk], k);
+            float sq = 0.f, sk = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                sq = __builtin_fmaf(q[i], q[i], sq);
+                sk = __builtin_fmaf(k[i], k[i], sk);
+            }
+            sq = row_sum16(sq);
+            sk = row_sum16(sk);
+            // sum / 128 is exact (a power of two)
+            const float iq = __builtin_amdgcn_rsqf(sq * (1.f / (float)HEAD_D) + a.eps) * a.qscale;
+            const float ik = __builtin_amdgcn_rsqf(sk * (1.f / (float)HEAD_D) + a.eps);
+            const float csv[8] = {cs[kk][0].x, cs[kk][0].y, cs[kk][0].z, cs[kk][0].w,
+                                  cs[kk][1].x, cs[kk][1].y, cs[kk][1].z, cs[kk][1].w};
+            rope8(q, gqv, iq, csv);
+            rope8(k, gkv, ik, csv);
+            IO::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
+            IO::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s) {
-    const dim3 grid(xcd_grid((long)a.n_tiles * HEADS)), block(256);
+    const dim3 block(256);
     if (dtype == AWA_BF16)
-        hipLaunchKernelGGL((pack_kernel<uint16_t, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL(pack_bf16_kernel, dim3(xcd_grid((long)a.n_tiles * (HEADS / PACK_HG))), block, 0, s, a);
     else
-        hipLaunchKernelGGL((pack_kernel<float, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((pack_kernel<float, true>), dim3(xcd_grid((long)a.n_tiles * HEADS)), block, 0, s, a);
     return hipGetLastError();
 }
 

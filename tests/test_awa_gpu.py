@@ -422,3 +422,19 @@ def test_geometry_from_win_rejects(oracle, ctx, awa):
     sl[1] = [s0[0], s0[0] + 1, s0[2], s0[2] + 1, s0[4], s0[4] + 1]  # window 0's first token again
     with pytest.raises(awa.AwaError, match="two windows"):
         ctx.geometry_from_win(1, 23, 27, sl, vf_for(sl), og.txt_freq, 58)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 16, (56 << 20) + 48])
+def test_stream_copy(ctx, awa, nbytes):
+    """awa_stream_copy (the measuring copy) moves every byte, including a
+    partial last block, and rejects sizes that are not multiples of 16."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(nbytes)
+    src = torch.randint(0, 255, (nbytes,), generator=g, device=dev, dtype=torch.uint8)
+    dst = torch.zeros_like(src)
+    ctx.stream_copy(src, dst)
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    with pytest.raises(awa.AwaError):
+        ctx.stream_copy(src[:-8], dst[:-8])
