@@ -89,7 +89,7 @@ hipError_t dalloc(T** p, size_t n) {
 
 void free_geom_buffers(awa_geom* g) {
     void* ptrs[] = {g->d_slices, g->d_cumf, g->d_vidx, g->d_tile_base, g->d_tile_win,
-                    g->d_items, g->d_sched_start, g->d_sched_desc, g->d_vfreq, g->d_tfreq,
+                    g->d_items, g->d_f32_units, g->d_sched_start, g->d_sched_desc, g->d_vfreq, g->d_tfreq,
                     g->d_vcs, g->d_tcs, g->d_tile_meta, g->d_vrow};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -137,6 +137,17 @@ void plan_tiles(GeomPlan& P) {
         }
     }
     P.n_items = (int)P.items.size() / 4;
+    // fp32 units: every query tile of every item, longest windows first
+    std::vector<int> units;
+    for (int i = 0; i < P.n_items; i++)
+        for (int half = 0; half < 2; half++)
+            if (P.items[4 * i + 1 + half] >= 0) units.push_back(2 * i + half);
+    auto nkey = [&](int u) {
+        const int w = P.items[4 * (u >> 1)];
+        return P.tile_base[w + 1] - P.tile_base[w];
+    };
+    std::stable_sort(units.begin(), units.end(), [&](int x, int y) { return nkey(x) > nkey(y); });
+    P.f32_units.assign(units.begin(), units.end());
 }
 
 // Static schedule of the persistent bf16 attention
@@ -277,6 +288,10 @@ int upload_plan(awa_ctx* ctx, awa_geom* g, hipStream_t s) {
     HIPCK(ctx, dalloc(&g->d_tile_base, P.tile_base.size()));
     HIPCK(ctx, dalloc(&g->d_tile_win, P.tile_win.size()));
     HIPCK(ctx, dalloc(&g->d_items, P.items.size()));
+    HIPCK(ctx, dalloc(&g->d_f32_units, P.f32_units.size()));
+    if (!P.f32_units.empty())
+        HIPCK(ctx, hipMemcpyAsync(g->d_f32_units, P.f32_units.data(), P.f32_units.size() * 4,
+                                  hipMemcpyHostToDevice, s));
     HIPCK(ctx, hipMemcpyAsync(g->d_tile_base, P.tile_base.data(), P.tile_base.size() * 4,
                               hipMemcpyHostToDevice, s));
     if (!P.tile_win.empty())
@@ -433,6 +448,7 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
     sa.n_vid_tiles = P.n_vid_tiles; sa.ntt = P.ntt; sa.txt_sets = P.txt_sets; sa.txt_len = P.txt_len;
     sa.n_tiles = P.n_tiles; sa.n_items = P.n_items; sa.nwin = P.nwin;
     sa.scale_log2e = 1.0f;  // the pack kernel folded the scale into Q
+    sa.f32_units = g->d_f32_units; sa.n_f32_units = (int)P.f32_units.size();
     HIPCK(ctx, launch_sdpa(dtype, sa, s));
     HIPCK(ctx, mark());
 

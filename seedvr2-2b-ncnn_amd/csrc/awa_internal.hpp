@@ -112,6 +112,11 @@ struct GeomPlan {
     std::vector<int32_t> tile_win;   // n_vid_tiles, window of each video tile
     std::vector<int32_t> tile_meta;  // n_tiles*2: RoPE-table row of slot 0, valid rows
     std::vector<int32_t> items;      // n_items*4: window, first q tile, second q tile (-1), 0
+    // Work units of the fp32 attention kernel (one workgroup per unit and
+    // head): 2 item + query tile of the item, units of windows with more key
+    // tiles first (workgroups are dispatched in index order, and window sizes
+    // can differ several-fold: the longest must start first).
+    std::vector<int32_t> f32_units;
     // Persistent schedule of the bf16 attention kernel: one workgroup per
     // resident slot (two per CU); slot s runs on XCD s % 8 and processes the
     // work items sched_start[s] .. sched_start[s+1]) of sched_desc, longest
@@ -196,6 +201,7 @@ struct awa_geom {
     int32_t* d_tile_base = nullptr;
     int32_t* d_tile_win = nullptr;
     int32_t* d_items = nullptr;
+    int32_t* d_f32_units = nullptr;  // GeomPlan::f32_units
     int32_t* d_sched_start = nullptr;
     int32_t* d_sched_desc = nullptr;
     float* d_vfreq = nullptr;
@@ -289,6 +295,8 @@ struct SdpaArgs {
     float* tpart;          // [nwin][txt_len][2560] fp32 text partials
     int n_vid_tiles, ntt, txt_sets, txt_len, n_tiles, n_items, nwin;
     float scale_log2e;     // multiplier of the scores (1 when Q carries the scale)
+    const int32_t* f32_units;  // fp32 kernel: GeomPlan::f32_units
+    int n_f32_units;
 };
 hipError_t launch_sdpa(int dtype, const SdpaArgs& a, hipStream_t s);
 hipError_t launch_sdpa_f32(const SdpaArgs& a, hipStream_t s);   // awa_sdpa_f32.hip

@@ -46,64 +46,15 @@ __device__ inline WinTiles window_tiles(const SdpaArgs& a, int w) {
 // a contiguous range of (head, item) ids: consecutive items of one head are
 // mostly the same window and share its K/V tiles through that XCD's L2.
 
-// Online-softmax update of one 64-key tile held as two 32x32 S^T accumulators
-// (lane: query column n = lane % 32; register r: key 8(r/4) + 4(lane/32) + r%4
-// of each 32-key half).  Scales and masks the scores, returns the factor that
-// rescales the running output, and leaves exp2(s - m) in sacc.
-__device__ inline float softmax_tile(f32x16 (&sacc)[2], int kvalid, int hb, float scale,
-                                     float& m_i, float& l_i) {
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = 32 * kt + 8 * (r >> 2) + 4 * hb + (r & 3);
-            const float v = key < kvalid ? sacc[kt][r] * scale : -INFINITY;
-            sacc[kt][r] = v;
-            mloc = fmaxf(mloc, v);
-        }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_i, mloc);  // finite: every tile has a valid key
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(sacc[kt][r] - m_new);
-            sacc[kt][r] = p;
-            psum += p;
-        }
-    l_i = l_i * alpha + psum;
-    m_i = m_new;
-    return alpha;
-}
-
-// Writes the normalised O^T accumulators of one wave (lane: query n, register
-// r of d-tile dt: channel 32dt + 8(r/4) + 4(lane/32) + r%4).
-__device__ inline void store_rows(const f32x16 (&oacc)[4], float inv, int hb, float* dst_row) {
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int d0 = 32 * dt + 8 * g + 4 * hb;
-            *reinterpret_cast<float4*>(dst_row + d0) =
-                make_float4(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv, oacc[dt][4 * g + 2] * inv,
-                            oacc[dt][4 * g + 3] * inv);
-        }
-}
-
 // Destination of query slot `slot` of query tile kq (nullptr: padding slot).
 __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, int h, int kq,
-                                  int slot, bool& to_text, size_t elem) {
+                                  int slot, size_t elem) {
     if (slot >= wt.nvalid(kq)) return nullptr;
     if (kq < wt.nvt) {
-        to_text = false;
         const int g = a.cumf[w] + TILE * kq + slot;
         const size_t tok = (size_t)a.vidx[g];
         return reinterpret_cast<char*>(a.vattn) + (tok * DIM + (size_t)h * HEAD_D) * elem;
     }
-    to_text = true;
     const int i = TILE * (kq - wt.nvt) + slot;
     return a.tpart + ((size_t)w * a.txt_len + i) * DIM + (size_t)h * HEAD_D;
 }
@@ -111,166 +62,176 @@ __device__ inline void* query_dst(const SdpaArgs& a, const WinTiles& wt, int w, 
 constexpr int KP32 = 132;                 // LDS pitch of a K row (floats)
 constexpr int VP32 = 68;                  // LDS pitch of a V^T row (floats)
 constexpr int KS32 = TILE * KP32;
-constexpr int STAGE32 = KS32 + HEAD_D * VP32;
+constexpr int STAGE32 = KS32 + HEAD_D * VP32;  // one K and one V^T tile: 68.6 KiB
 
-__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void sdpa_f32_kernel(SdpaArgs a) {
-    __shared__ __align__(16) float lds[2 * STAGE32];
-    const int nblk = a.n_items * HEADS;
-    const int lid = xcd_remap(nblk);
-    if (lid >= nblk) return;
-    const int h = lid / a.n_items;
-    const int item = lid % a.n_items;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-    const int4 it = reinterpret_cast<const int4*>(a.items)[item];
+// One workgroup (4 wave64) per (64-row query tile, head); wave q owns the
+// tile's queries 16 q .. 16 q + 15.  With v_mfma_f32_16x16x4_f32 a wave
+// holds its Q (32 floats), O^T (32) and one key tile's scores (16) in few
+// registers, so two workgroups share a CU (one LDS tile stage each, 68.6 KiB):
+// while one waits for its next tile or sits at a barrier, the other's MFMAs
+// run on the same SIMDs.
+//
+// Lane l = 16 g + j (j: the lane's query; g: its group of four).
+//   S^T = K Q^T per 16-key block kb and k-step s (32 steps of 4 channels):
+//     A: K[16 kb + j][32 g + s], B: Q[j][32 g + s] (step s pairs channel
+//     32 g + s across the four lane groups: any channel order that A and B
+//     share gives the same dot products), out: lane l holds keys
+//     16 kb + 4 g + r (r = 0..3) of query j.
+//   O^T += V^T P^T per 16-channel block db and key step (kb, r):
+//     A: V^T[16 db + j][16 kb + 4 g + r], B: P[j][16 kb + 4 g + r], which is
+//     exactly score register r of block kb: the probabilities never move.
+//     out: lane l holds channels 16 db + 4 g + r of query j.
+// A query's scores are spread over lanes j, j + 16, j + 32, j + 48: its row
+// maximum and sum take two cross-lane steps.
+__global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
+    __shared__ __align__(16) float lds[STAGE32];
+    // Workgroup b: head b % 20 of query tile GeomPlan::f32_units[b / 20]
+    // (2 item + tile of the item), the tiles of windows with more key tiles
+    // first: workgroups are dispatched in index order, and window sizes can
+    // differ several-fold (the slowest workgroup sets the time).
+    const int lid = (int)blockIdx.x;
+    if (lid >= a.n_f32_units * HEADS) return;
+    const int h = lid % HEADS;
+    const int unit = a.f32_units[lid / HEADS];
+    const int4 it = reinterpret_cast<const int4*>(a.items)[unit >> 1];
+    const int kq = (unit & 1) ? it.z : it.y;
     const int w = it.x;
     const WinTiles wt = window_tiles(a, w);
     const int nk = wt.nvt + wt.ntt;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n = lane & 31, hb = lane >> 5;
-    const int kq = wave < 2 ? it.y : it.z;
-    const bool active = kq >= 0;
-    const int qslot = (wave & 1) * 32 + n;
+    const int j = lane & 15, g = lane >> 4;
+    const int qslot = 16 * wave + j;
 
     const size_t head_off = (size_t)h * a.n_tiles * TILE * HEAD_D;
     const float* Qh = reinterpret_cast<const float*>(a.Qp) + head_off;
     const float* Kh = reinterpret_cast<const float*>(a.Kp) + head_off;
     const float* Vh = reinterpret_cast<const float*>(a.Vp) + head_off;
 
-    // k-step s of S^T pairs channel s (lanes 0-31) with channel 64 + s
-    // (lanes 32-63): lane (n, hb) holds Q[slot][64hb + s].
-    // Loaded on every path (an idle wave reads its partner's tile): a load
-    // under a condition leaves the array to scratch memory.
-    float qf[64];
+    // B operand of S^T: Q[qslot][32 g + s], s = 0..31
+    float qf[32];
     {
-        const float* qrow = Qh + ((size_t)wt.tile(active ? kq : it.y) * TILE + qslot) * HEAD_D + 64 * hb;
+        const float* qrow = Qh + ((size_t)wt.tile(kq) * TILE + qslot) * HEAD_D + 32 * g;
 #pragma unroll
-        for (int s = 0; s < 64; s += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(qrow + s);
-            qf[s] = v.x; qf[s + 1] = v.y; qf[s + 2] = v.z; qf[s + 3] = v.w;
+        for (int s = 0; s < 32; s += 4) {
+            const f32x4v v = *reinterpret_cast<const f32x4v*>(qrow + s);
+            qf[s] = v[0]; qf[s + 1] = v[1]; qf[s + 2] = v[2]; qf[s + 3] = v[3];
         }
     }
 
-    // K and V tiles go through the same 32 staging registers one after the
-    // other: K of the next tile is loaded at the top of an iteration and
-    // stored to the free LDS stage after the score MFMAs, V is loaded then
-    // and stored at the end (two staging sets at once made the kernel spill).
-    // (a plain vector type: an array of HIP's float4 stayed in scratch memory)
-    f32x4 reg[8];
-    auto load_k = [&](int kk) __attribute__((always_inline)) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(Kh + (size_t)wt.tile(kk) * TILE * HEAD_D);
-#pragma unroll
-        for (int i = 0; i < 8; i++) reg[i] = src[tid + 256 * i];
-    };
-    auto load_v = [&](int kk) __attribute__((always_inline)) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(Vh + (size_t)wt.tile(kk) * TILE * HEAD_D);
-#pragma unroll
-        for (int i = 0; i < 8; i++) reg[i] = src[tid + 256 * i];
-    };
-    auto store_k = [&](int stage) __attribute__((always_inline)) {
-        float* ks = lds + stage * STAGE32;
+    // The next tile's K and V^T travel through registers (eight 16-byte
+    // pieces of each per thread) while the current tile is computed.
+    f32x4v rk[8], rv[8];
+    auto load_tile = [&](int kk) __attribute__((always_inline)) {
+        const size_t t = (size_t)wt.tile(kk) * TILE * HEAD_D;
+        const f32x4v* ks = reinterpret_cast<const f32x4v*>(Kh + t);
+        const f32x4v* vs = reinterpret_cast<const f32x4v*>(Vh + t);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<f32x4*>(ks + (c >> 5) * KP32 + (c & 31) * 4) = reg[i];
+            rk[i] = ks[tid + 256 * i];
+            rv[i] = vs[tid + 256 * i];
         }
     };
-    auto store_v = [&](int stage) __attribute__((always_inline)) {
-        float* vs = lds + stage * STAGE32 + KS32;
+    auto store_tile = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<f32x4*>(vs + (c >> 4) * VP32 + (c & 15) * 4) = reg[i];
+            *reinterpret_cast<f32x4v*>(lds + (c >> 5) * KP32 + (c & 31) * 4) = rk[i];      // K row c / 32
+            *reinterpret_cast<f32x4v*>(lds + KS32 + (c >> 4) * VP32 + (c & 15) * 4) = rv[i];  // V^T row c / 16
         }
     };
 
-    f32x16 oacc[4];
+    f32x4v oacc[8];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) oacc[dt][r] = 0.f;
+    for (int db = 0; db < 8; db++) oacc[db] = (f32x4v){0.f, 0.f, 0.f, 0.f};
     float m_i = -INFINITY, l_i = 0.f;
 
-    load_k(0);
-    store_k(0);
-    load_v(0);
-    store_v(0);
+    load_tile(0);
+    store_tile();
     __syncthreads();
     for (int kk = 0; kk < nk; kk++) {
-        const int stage = kk & 1;
-        if (kk + 1 < nk) load_k(kk + 1);
-        if (active) {
-            const float* ks = lds + stage * STAGE32;
-            const float* vs = ks + KS32;
-            f32x16 sacc[2];
+        if (kk + 1 < nk) load_tile(kk + 1);
+        // ---- scores of the tile: four 16-key blocks
+        f32x4v sacc[4];
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+        for (int kb = 0; kb < 4; kb++) {
+            sacc[kb] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+            const float* krow = lds + (16 * kb + j) * KP32 + 32 * g;
 #pragma unroll
-                for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
+            for (int s = 0; s < 32; s += 4) {
+                const f32x4v kv = *reinterpret_cast<const f32x4v*>(krow + s);
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const float* krow = ks + (32 * kt + n) * KP32 + 64 * hb;
-#pragma unroll
-                for (int s = 0; s < 64; s += 4) {
-                    const float4 kv = *reinterpret_cast<const float4*>(krow + s);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[s], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[s + 1], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[s + 2], sacc[kt], 0, 0, 0);
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[s + 3], sacc[kt], 0, 0, 0);
-                }
+                for (int e = 0; e < 4; e++)
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qf[s + e], sacc[kb], 0, 0, 0);
             }
-            if (kk + 1 < nk) {
-                store_k(stage ^ 1);
-                load_v(kk + 1);
+        }
+        // ---- online softmax (scale folded into Q; keys past the tile's
+        // valid count get -inf)
+        const int kvalid = wt.nvalid(kk);
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = 16 * kb + 4 * g + r;
+                const float v = key < kvalid ? sacc[kb][r] * a.scale_log2e : -INFINITY;
+                sacc[kb][r] = v;
+                mloc = fmaxf(mloc, v);
             }
-            const float alpha = softmax_tile(sacc, wt.nvalid(kk), hb, a.scale_log2e, m_i, l_i);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        const float m_new = fmaxf(m_i, mloc);  // finite: every tile has a valid key
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+        float psum = 0.f;
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++)
+        for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) oacc[dt][r] *= alpha;
-            // O^T += V^T P^T; k-step r pairs key 8(r/4)+r%4 (lanes 0-31) with
-            // key 8(r/4)+4+r%4 (lanes 32-63) of the 32-key half kt, which is
-            // exactly where the S^T accumulator left P.
+            for (int r = 0; r < 4; r++) {
+                const float p = __builtin_amdgcn_exp2f(sacc[kb][r] - m_new);
+                sacc[kb][r] = p;
+                psum += p;
+            }
+        l_i = l_i * alpha + psum;  // this lane's keys; summed over the group at the end
+        m_i = m_new;
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+        for (int db = 0; db < 8; db++) oacc[db] *= alpha;
+        // ---- O^T += V^T P^T
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const float* vrow = vs + (32 * dt + n) * VP32 + 32 * kt + 4 * hb;
+        for (int db = 0; db < 8; db++) {
+            const float* vrow = lds + KS32 + (16 * db + j) * VP32 + 4 * g;
 #pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const float4 vv = *reinterpret_cast<const float4*>(vrow + 8 * g);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sacc[kt][4 * g], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sacc[kt][4 * g + 1], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, sacc[kt][4 * g + 2], oacc[dt], 0, 0, 0);
-                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, sacc[kt][4 * g + 3], oacc[dt], 0, 0, 0);
-                    }
-                }
+            for (int kb = 0; kb < 4; kb++) {
+                const f32x4v vv = *reinterpret_cast<const f32x4v*>(vrow + 16 * kb);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r], sacc[kb][r], oacc[db], 0, 0, 0);
+            }
         }
         if (kk + 1 < nk) {
-            if (!active) {  // idle waves still carry their share of the tiles
-                store_k(stage ^ 1);
-                load_v(kk + 1);
-            }
-            store_v(stage ^ 1);
+            __syncthreads();  // every wave is done with this tile
+            store_tile();
+            __syncthreads();
         }
-        __syncthreads();
     }
-    if (!active) return;
-    const float l = l_i + __shfl_xor(l_i, 32);
+    float l = l_i + __shfl_xor(l_i, 16);
+    l += __shfl_xor(l, 32);
     const float inv = 1.f / l;
-    bool to_text = false;
-    void* dst = query_dst(a, wt, w, h, kq, qslot, to_text, 4);
+    float* dst = reinterpret_cast<float*>(query_dst(a, wt, w, h, kq, qslot, 4));
     if (dst == nullptr) return;
-    store_rows(oacc, inv, hb, reinterpret_cast<float*>(dst));
+#pragma unroll
+    for (int db = 0; db < 8; db++)
+        *reinterpret_cast<float4*>(dst + 16 * db + 4 * g) =
+            make_float4(oacc[db][0] * inv, oacc[db][1] * inv, oacc[db][2] * inv, oacc[db][3] * inv);
 }
 
 }  // namespace
 
 hipError_t launch_sdpa_f32(const SdpaArgs& a, hipStream_t s) {
-    const int nblk = a.n_items * HEADS;
-    const int grid = ((nblk + 7) >> 3) << 3;
-    hipLaunchKernelGGL(sdpa_f32_kernel, dim3(grid), dim3(256), 0, s, a);
+    const int nblk = a.n_f32_units * HEADS;
+    if (nblk == 0) return hipSuccess;
+    hipLaunchKernelGGL(sdpa_f32_kernel, dim3(nblk), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

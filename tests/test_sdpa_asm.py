@@ -248,7 +248,8 @@ def test_m0_written_only_by_the_kernels_asm(sdpa_asm):
 # source read of a v_mfma_f32_32x32x16_bf16 result 12 (s_nop 11), of a
 # v_mfma_f32_16x16x32_bf16 result 8, of a v_mfma_f32_32x32x2_f32 result 18;
 # a read of a transcendental result one.
-MFMA_READ_WAIT = {"v_mfma_f32_32x32x16_bf16": 12, "v_mfma_f32_16x16x32_bf16": 8, "v_mfma_f32_32x32x2_f32": 18}
+MFMA_READ_WAIT = {"v_mfma_f32_32x32x16_bf16": 12, "v_mfma_f32_16x16x32_bf16": 8, "v_mfma_f32_32x32x2_f32": 18,
+                  "v_mfma_f32_16x16x4_f32": 10}
 TRANS_READ_WAIT = 1
 VREG = re.compile(r"\b([va])\[(\d+):(\d+)\]|\b([va])(\d+)\b")
 TRANS = re.compile(r"^v_(exp|log|rcp|rsq|sqrt|sin|cos)_f32")
@@ -323,6 +324,12 @@ def wait_state_violations(insts):
             if op == "s_nop":
                 n = int(rest.split()[0], 0) + 1
             state = {r: w - n for r, w in state.items() if w - n > 0}
+            # a register another instruction writes no longer holds the result
+            if ops and not op.startswith("v_mfma") and (op.startswith("v_") or op.startswith("ds_read")
+                                                         or op.startswith("global_load")
+                                                         or (op.startswith("buffer_load") and "lds" not in rest)):
+                for r in vregs(ops[0]):
+                    state.pop(r, None)
             if op.startswith("v_mfma") and ops:
                 for r in vregs(ops[0]):
                     state[r] = MFMA_READ_WAIT.get(op, 18)
