@@ -12,7 +12,8 @@ pressure), the use would read stale data without any error.  This test
 compiles the kernel to AMD assembly with the library's own flags (Makefile)
 and proves on its control-flow graph that on every path from such a load no
 instruction touches the loaded registers before a wait that covers it
-(`vmcnt(0)` for vector memory loads, `lgkmcnt(0)` for LDS reads).  The
+(`vmcnt(N)` with at least N vector memory instructions issued after the load
+on every path, `lgkmcnt(0)` for LDS reads).  The
 analysis is checked on planted mistakes first.  A second
 check: the kernel's LDS DMA takes its destination from M0, written by the
 kernel's asm once per four DMA instructions, so no compiler-generated
@@ -37,6 +38,7 @@ AREG = re.compile(r"\ba\[(\d+):(\d+)\]|\ba(\d+)\b")
 LABEL = re.compile(r"^(\.LBB\d+_\d+):")
 VMEM_LOAD = re.compile(r"^(global|buffer|flat)_load_")
 LDS_LOAD = re.compile(r"^ds_read")
+VMEM_ANY = re.compile(r"^(global|buffer|flat|scratch)_")
 
 
 def makefile_flags():
@@ -118,23 +120,44 @@ def check(insts, load=VMEM_LOAD, wait=r"vmcnt\(0\)"):
                 s.append(nxt)
         succ[b] = [x for x in s if x in blocks]
     n_loads = sum(1 for b in order for op, rest in blocks[b] if load.match(op) and rest.startswith("a"))
-    pend_in = {b: set() for b in order}
+    # pending: loaded register -> vector memory instructions issued since its
+    # load (the fewest over the paths that reach here).  Vector memory
+    # operations complete in issue order, so `s_waitcnt vmcnt(N)` covers a
+    # load with at least N such instructions after it; for LDS reads (whose
+    # counter SMEM shares, out of order) only a full wait counts.
+    counted = load is VMEM_LOAD
+    pend_in = {b: {} for b in order}
     violations = []
 
     def run(b, pending, record):
-        pending = set(pending)
+        pending = dict(pending)
         for op, rest in blocks[b]:
-            if op == "s_waitcnt" and re.search(wait, rest):
-                pending.clear()
+            if op == "s_waitcnt":
+                if re.search(wait, rest):
+                    pending.clear()
+                    continue
+                m = re.search(r"vmcnt\((\d+)\)", rest)
+                if counted and m:
+                    n = int(m.group(1))
+                    pending = {r: c for r, c in pending.items() if c < n}
                 continue
             r = regs(rest)
             if load.match(op) and rest.startswith("a"):
-                pending |= r
+                for x in r:
+                    pending[x] = 0
                 continue
-            hit = r & pending
+            hit = r & set(pending)
             if hit and record:
                 violations.append((b, f"{op} {rest}", sorted(hit)))
+            if counted and VMEM_ANY.match(op):
+                pending = {x: c + 1 for x, c in pending.items()}
         return pending
+
+    def merge(into, new):
+        out = dict(into)
+        for x, c in new.items():
+            out[x] = min(c, out[x]) if x in out else c
+        return out
 
     changed = True
     while changed:
@@ -142,8 +165,9 @@ def check(insts, load=VMEM_LOAD, wait=r"vmcnt\(0\)"):
         for b in order:
             out = run(b, pend_in[b], False)
             for s in succ[b]:
-                if not out <= pend_in[s]:
-                    pend_in[s] |= out
+                m = merge(pend_in[s], out)
+                if m != pend_in[s]:
+                    pend_in[s] = m
                     changed = True
     for b in order:
         run(b, pend_in[b], True)
@@ -183,6 +207,18 @@ def test_analysis_finds_planted_uses(sdpa_asm):
                                (None, "v_mov_b32", f"v1, a{reg}")] + insts[k + 1:]
     v3, _ = check(branchy)
     assert any("v1, a%d" % reg in ins for _, ins, _ in v3)
+    # a count-based wait covers the load only with that many vector memory
+    # instructions issued after it
+    short = insts[:k + 1] + [(None, "global_store_dwordx4", "v0, v[0:3], off"),
+                             (None, "s_waitcnt", "vmcnt(2)"), (None, "v_accvgpr_read_b32", f"v0, a{reg}")] + insts[k + 1:]
+    v4, _ = check(short)
+    assert any("v0, a%d" % reg in ins for _, ins, _ in v4)
+    enough = insts[:k + 1] + [(None, "global_store_dwordx4", "v0, v[0:3], off"),
+                              (None, "global_store_dwordx4", "v0, v[0:3], off offset:16"),
+                              (None, "s_waitcnt", "vmcnt(2)"), (None, "v_accvgpr_read_b32", f"v0, a{reg}")] + \
+        insts[k + 1:]
+    v5, _ = check(enough)
+    assert not any("v0, a%d" % reg in ins for _, ins, _ in v5)
 
 
 def test_query_fragment_loads_are_waited_for(sdpa_asm):
