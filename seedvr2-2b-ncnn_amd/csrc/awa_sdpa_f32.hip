@@ -66,12 +66,18 @@ constexpr int STAGE32 = KS32 + HEAD_D * VP32;  // one K and one V^T tile: 68.6 K
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-// One workgroup (4 wave64) per (64-row query tile, head); wave q owns the
-// tile's queries 16 q .. 16 q + 15.  With v_mfma_f32_16x16x4_f32 a wave
-// holds its Q (32 floats), O^T (32) and one key tile's scores (16) in few
-// registers, so two workgroups share a CU (one LDS tile stage each, 68.6 KiB):
-// while one waits for its next tile or sits at a barrier, the other's MFMAs
-// run on the same SIMDs.
+// One workgroup per (64-row query tile, head).  With v_mfma_f32_16x16x4_f32 a
+// wave holds 16 queries' Q (32 floats), O^T (32) and one key tile's scores (16)
+// in few registers, so two waves share each SIMD:
+//   kSplit = false: four waves (wave w owns the tile's queries 16 w .. + 15)
+//     and one LDS tile stage (68.6 KiB): two workgroups per CU;
+//   kSplit = true: eight waves in two halves of four, half 0 taking the
+//     window's key tiles [0, nk0), half 1 the rest (nk0 = ceil(nk / 2)), each
+//     through its own stage: one workgroup per CU, and a long window's key
+//     tiles take half as long; at the end half 1 leaves its row maxima, sums
+//     and O^T in its stage and half 0 merges them.
+// The launch takes the split form for small grids (at most two workgroups per
+// CU, where the longest query tile sets the time), else the other.
 //
 // Lane l = 16 g + j (j: the lane's query; g: its group of four).
 //   S^T = K Q^T per 16-key block kb and k-step s (32 steps of 4 channels):
@@ -85,8 +91,10 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 //     out: lane l holds channels 16 db + 4 g + r of query j.
 // A query's scores are spread over lanes j, j + 16, j + 32, j + 48: its row
 // maximum and sum take two cross-lane steps.
-__global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
-    __shared__ __align__(16) float lds[STAGE32];
+template <bool kSplit>
+__global__ __launch_bounds__(kSplit ? 512 : 256, 2) void sdpa_f32_kernel(SdpaArgs a) {
+    constexpr int HALVES = kSplit ? 2 : 1;
+    __shared__ __align__(16) float lds[HALVES * STAGE32];
     // Workgroup b: head b % 20 of query tile GeomPlan::f32_units[b / 20]
     // (2 item + tile of the item), the tiles of windows with more key tiles
     // first: workgroups are dispatched in index order, and window sizes can
@@ -102,8 +110,13 @@ __global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
     const int nk = wt.nvt + wt.ntt;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int half = kSplit ? __builtin_amdgcn_readfirstlane(wave >> 2) : 0;
+    const int htid = tid & 255;  // thread index within the half
     const int j = lane & 15, g = lane >> 4;
-    const int qslot = 16 * wave + j;
+    const int qslot = 16 * (wave & 3) + j;
+    float* stage = lds + half * STAGE32;
+    const int nk0 = kSplit ? (nk + 1) >> 1 : nk;  // iterations: half 0 has nk0 tiles, half 1 nk - nk0
+    const int kbeg = half ? nk0 : 0, kend = half ? nk : nk0;
 
     const size_t head_off = (size_t)h * a.n_tiles * TILE * HEAD_D;
     const float* Qh = reinterpret_cast<const float*>(a.Qp) + head_off;
@@ -121,8 +134,8 @@ __global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
         }
     }
 
-    // The next tile's K and V^T travel through registers (eight 16-byte
-    // pieces of each per thread) while the current tile is computed.
+    // The half's next tile's K and V^T travel through registers (eight
+    // 16-byte pieces of each per thread) while its current tile is computed.
     f32x4v rk[8], rv[8];
     auto load_tile = [&](int kk) __attribute__((always_inline)) {
         const size_t t = (size_t)wt.tile(kk) * TILE * HEAD_D;
@@ -130,16 +143,16 @@ __global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
         const f32x4v* vs = reinterpret_cast<const f32x4v*>(Vh + t);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            rk[i] = ks[tid + 256 * i];
-            rv[i] = vs[tid + 256 * i];
+            rk[i] = ks[htid + 256 * i];
+            rv[i] = vs[htid + 256 * i];
         }
     };
     auto store_tile = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<f32x4v*>(lds + (c >> 5) * KP32 + (c & 31) * 4) = rk[i];      // K row c / 32
-            *reinterpret_cast<f32x4v*>(lds + KS32 + (c >> 4) * VP32 + (c & 15) * 4) = rv[i];  // V^T row c / 16
+            const int c = htid + 256 * i;
+            *reinterpret_cast<f32x4v*>(stage + (c >> 5) * KP32 + (c & 31) * 4) = rk[i];      // K row c / 32
+            *reinterpret_cast<f32x4v*>(stage + KS32 + (c >> 4) * VP32 + (c & 15) * 4) = rv[i];  // V^T row c / 16
         }
     };
 
@@ -148,75 +161,106 @@ __global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
     for (int db = 0; db < 8; db++) oacc[db] = (f32x4v){0.f, 0.f, 0.f, 0.f};
     float m_i = -INFINITY, l_i = 0.f;
 
-    load_tile(0);
-    store_tile();
+    if (kbeg < kend) {
+        load_tile(kbeg);
+        store_tile();
+    }
     __syncthreads();
-    for (int kk = 0; kk < nk; kk++) {
-        if (kk + 1 < nk) load_tile(kk + 1);
-        // ---- scores of the tile: four 16-key blocks
-        f32x4v sacc[4];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            sacc[kb] = (f32x4v){0.f, 0.f, 0.f, 0.f};
-            const float* krow = lds + (16 * kb + j) * KP32 + 32 * g;
-#pragma unroll
-            for (int s = 0; s < 32; s += 4) {
-                const f32x4v kv = *reinterpret_cast<const f32x4v*>(krow + s);
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qf[s + e], sacc[kb], 0, 0, 0);
-            }
-        }
-        // ---- online softmax (scale folded into Q; keys past the tile's
-        // valid count get -inf)
-        const int kvalid = wt.nvalid(kk);
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = 16 * kb + 4 * g + r;
-                const float v = key < kvalid ? sacc[kb][r] * a.scale_log2e : -INFINITY;
-                sacc[kb][r] = v;
-                mloc = fmaxf(mloc, v);
-            }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_i, mloc);  // finite: every tile has a valid key
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-        float psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float p = __builtin_amdgcn_exp2f(sacc[kb][r] - m_new);
-                sacc[kb][r] = p;
-                psum += p;
-            }
-        l_i = l_i * alpha + psum;  // this lane's keys; summed over the group at the end
-        m_i = m_new;
-#pragma unroll
-        for (int db = 0; db < 8; db++) oacc[db] *= alpha;
-        // ---- O^T += V^T P^T
-#pragma unroll
-        for (int db = 0; db < 8; db++) {
-            const float* vrow = lds + KS32 + (16 * db + j) * VP32 + 4 * g;
+    for (int i = 0; i < nk0; i++) {  // the same iteration count in both halves
+        const int kk = kbeg + i;
+        const bool have = kk < kend, have_next = kk + 1 < kend;  // uniform per half
+        if (have_next) load_tile(kk + 1);
+        if (have) {
+            // ---- scores of the tile: four 16-key blocks
+            f32x4v sacc[4];
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
-                const f32x4v vv = *reinterpret_cast<const f32x4v*>(vrow + 16 * kb);
+                sacc[kb] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+                const float* krow = stage + (16 * kb + j) * KP32 + 32 * g;
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r], sacc[kb][r], oacc[db], 0, 0, 0);
+                for (int s = 0; s < 32; s += 4) {
+                    const f32x4v kv = *reinterpret_cast<const f32x4v*>(krow + s);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qf[s + e], sacc[kb], 0, 0, 0);
+                }
+            }
+            // ---- online softmax (scale folded into Q; keys past the tile's
+            // valid count get -inf)
+            const int kvalid = wt.nvalid(kk);
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = 16 * kb + 4 * g + r;
+                    const float v = key < kvalid ? sacc[kb][r] * a.scale_log2e : -INFINITY;
+                    sacc[kb][r] = v;
+                    mloc = fmaxf(mloc, v);
+                }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            const float m_new = fmaxf(m_i, mloc);  // finite: every tile has a valid key
+            const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+            float psum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = __builtin_amdgcn_exp2f(sacc[kb][r] - m_new);
+                    sacc[kb][r] = p;
+                    psum += p;
+                }
+            l_i = l_i * alpha + psum;  // this lane's keys; summed over the group at the end
+            m_i = m_new;
+#pragma unroll
+            for (int db = 0; db < 8; db++) oacc[db] *= alpha;
+            // ---- O^T += V^T P^T
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                const float* vrow = stage + KS32 + (16 * db + j) * VP32 + 4 * g;
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const f32x4v vv = *reinterpret_cast<const f32x4v*>(vrow + 16 * kb);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r], sacc[kb][r], oacc[db], 0, 0, 0);
+                }
             }
         }
-        if (kk + 1 < nk) {
-            __syncthreads();  // every wave is done with this tile
-            store_tile();
+        if (i + 1 < nk0) {
+            __syncthreads();  // every wave is done with its half's tile
+            if (have_next) store_tile();
             __syncthreads();
         }
     }
     float l = l_i + __shfl_xor(l_i, 16);
     l += __shfl_xor(l, 32);
+    if constexpr (kSplit) {
+        // merge: half 1 leaves its running maximum (-inf when it had no
+        // tile), sum and O^T in its stage, half 0 rescales both to the common
+        // maximum
+        __syncthreads();
+        float* pub = lds + STAGE32;
+        if (half == 1) {
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+                *reinterpret_cast<f32x4v*>(pub + qslot * HEAD_D + 16 * db + 4 * g) = oacc[db];
+            if (g == 0) {
+                pub[TILE * HEAD_D + qslot] = m_i;
+                pub[TILE * HEAD_D + TILE + qslot] = l;
+            }
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = pub[TILE * HEAD_D + qslot], l1 = pub[TILE * HEAD_D + TILE + qslot];
+        const float m = fmaxf(m_i, m1);
+        const float a0 = __builtin_amdgcn_exp2f(m_i - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
+        l = l * a0 + l1 * a1;
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+            oacc[db] = oacc[db] * a0 + *reinterpret_cast<const f32x4v*>(pub + qslot * HEAD_D + 16 * db + 4 * g) * a1;
+    }
     const float inv = 1.f / l;
     float* dst = reinterpret_cast<float*>(query_dst(a, wt, w, h, kq, qslot, 4));
     if (dst == nullptr) return;
@@ -231,7 +275,13 @@ __global__ __launch_bounds__(256, 2) void sdpa_f32_kernel(SdpaArgs a) {
 hipError_t launch_sdpa_f32(const SdpaArgs& a, hipStream_t s) {
     const int nblk = a.n_f32_units * HEADS;
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL(sdpa_f32_kernel, dim3(nblk), dim3(256), 0, s, a);
+    // n_slots: two per CU (the persistent bf16 schedule's slot count); the
+    // split form at most two workgroups per CU (measured: 360p 63 -> 53 us,
+    // while 720p and larger grids are faster with two 4-wave workgroups per CU)
+    if (nblk <= a.n_slots)
+        hipLaunchKernelGGL(sdpa_f32_kernel<true>, dim3(nblk), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL(sdpa_f32_kernel<false>, dim3(nblk), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
