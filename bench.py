@@ -527,7 +527,7 @@ def main():
     pack_avg_s = ms_pack * 1e-3 / calls
     traffic = measured_traffic()
     sdpa_bytes = traffic.get("sdpa_bf16_kernel", {}).get("total_bytes")
-    pack_bytes = traffic.get("pack_kernel", {}).get("total_bytes")
+    pack_bytes = traffic.get("pack_bf16_kernel", {}).get("total_bytes")
 
     out = {
         "metric": METRIC,
