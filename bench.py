@@ -9,7 +9,9 @@ shifted (25 windows) geometry, as even and odd DiT layers do; geometry is
 built once per resolution before timing, as the reference caches it.
 
 Prints one JSON line.  `value` is ms per AWA layer (wall clock over the
-timed steps, bracketed by device synchronisation).  `roofline` covers the
+timed steps, captured as one HIP graph of that many layers as the DiT
+forward captures its layers, bracketed by device synchronisation; the
+eager and graph-per-layer figures are reported beside it).  `roofline` covers the
 dominant kernel (window attention) from HIP events recorded on its stream
 during the timed steps.  `cpu_baseline` times the oracle's single-threaded
 restatement of the reference CPU attention (dit_vk.cpp:345-462) on one full
@@ -494,8 +496,31 @@ def main():
     for k in range(args.steps):
         graphs[k % 2].replay()
     torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_step_1 = (time.perf_counter() - t0) * 1e3 / args.steps
     del graphs
+    # The timed steps as one graph of `steps` layers (geometries alternating), the
+    # form the layers take inside the captured DiT forward: one graph launch for
+    # the stack, where a graph per layer adds the launch gap between replays
+    # (about 8 us, measured in the kernel trace) to every layer.  Its first replay
+    # must reproduce the eager outputs of the last step bit for bit.
+    g_stack = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_stack, stream=side):
+        for k in range(args.steps):
+            step(k)
+    vattn.zero_()
+    tattn.zero_()
+    torch.cuda.synchronize()
+    g_stack.replay()
+    torch.cuda.synchronize()
+    last = (args.steps - 1) % 2
+    assert torch.equal(vattn, outs_eager[last][0]) and torch.equal(tattn, outs_eager[last][1]), \
+        "stacked graph replay differs from eager"
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g_stack.replay()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    del g_stack
 
     # per-variant breakdown (separate short runs, events only)
     per_variant = {}
@@ -542,8 +567,11 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (q/k/v ~ N(0,1), gains 1+N(0,0.02), seed 2)",
-        "timing": "HIP graph replay of the layer's launches (as inside the captured DiT forward), "
-                  "the two geometries alternating; eager launches: eager_ms_per_layer",
+        "timing": "the timed steps captured as one HIP graph of `steps` layers, the two geometries "
+                  "alternating (the form the layers take inside the captured DiT forward), replayed "
+                  "once; one graph per layer replayed alternately: graph_per_layer_ms (adds the "
+                  "launch gap between graph replays to each layer); eager launches: eager_ms_per_layer",
+        "graph_per_layer_ms": round(ms_step_1, 4),
         "eager_ms_per_layer": round(ms_eager, 4),
         "geometry_build_ms": {"unshifted": round(geom_ms[0], 3), "shifted": round(geom_ms[1], 3),
                               "note": "once per resolution (host planner + geom_build_kernel), "
