@@ -12,8 +12,10 @@ Prints one JSON line.  `value` is ms per AWA layer (wall clock over the
 timed steps, captured as one HIP graph of that many layers as the DiT
 forward captures its layers, bracketed by device synchronisation; the
 eager and graph-per-layer figures are reported beside it).  `roofline` covers the
-dominant kernel (window attention) from HIP events recorded on its stream
-during the timed steps.  `cpu_baseline` times the oracle's single-threaded
+dominant kernel (window attention): HIP events on its stream around
+back-to-back launches of it on the same inputs, per geometry, mixed as in the
+timed steps (the per-phase events of the timed steps, which add a launch gap
+to every phase, give `frac_by_phase_events`).  `cpu_baseline` times the oracle's single-threaded
 restatement of the reference CPU attention (dit_vk.cpp:345-462) on one full
 unshifted 1080p layer.
 """
@@ -139,7 +141,9 @@ def config_runs(ctx, torch, steps, cpu=True):
         es = 4 if store == "f32" else 2
         peak = PEAK_FP32_TFLOPS if store == "f32" else PEAK_BF16_TFLOPS
         attn_s = ma * 1e-3 / c
-        tfl = fl / attn_s / 1e12
+        # the kernel's own time: back-to-back launches between two events
+        attn_k = ctx.time_attention(g, vq, tq, *gains, reps=max(4, steps), eps=1e-5, vattn=va, tattn=ta) * 1e-3
+        tfl = fl / attn_k / 1e12
         qk_bytes = 2 * (Lv + txt) * 2 * 2560 * es
         co_bytes = (g.info()["nwin"] + 1) * txt * 2560 * 4
         r = {"grid": list(grid), "num_windows": list(nw), "txt_len": txt, "shifted": bool(sh),
@@ -148,6 +152,8 @@ def config_runs(ctx, torch, steps, cpu=True):
                            "text_average": round(mt * 1e3 / c, 2)},
              "attention_roofline": {"bound": "mfma", "achieved": round(tfl, 1), "peak": peak,
                                     "unit": "TFLOP/s", "frac": round(tfl / peak, 4),
+                                    "avg_launch_us": round(attn_k * 1e6, 2),
+                                    "frac_by_phase_events": round(fl / attn_s / 1e12 / peak, 4),
                                     "gflop_per_launch": round(fl / 1e9, 3)},
              "hbm_qknorm_rope_frac": round(qk_bytes / (mp * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4),
              "hbm_text_average_frac": round(co_bytes / (mt * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4)}
@@ -545,7 +551,14 @@ def main():
     n_unsh = (args.steps + 1) // 2
     n_sh = args.steps // 2
     flops_timed = n_unsh * flops[0] + n_sh * flops[1]
-    attn_avg_s = ms_attn * 1e-3 / calls
+    attn_evt_s = ms_attn * 1e-3 / calls  # per-phase events: the launch gap after each event included
+    # the kernel's own time: HIP events around `steps` back-to-back launches of
+    # the attention kernel per geometry on its stream (awa_time_attention), the
+    # timed mix of the two geometries
+    reps = max(4, args.steps)
+    t_attn = [ctx.time_attention(geoms[k], vq, tq, *gains, reps=reps, eps=1e-5, vattn=vattn, tattn=tattn) * 1e-3
+              for k in range(2)]
+    attn_avg_s = (n_unsh * t_attn[0] + n_sh * t_attn[1]) / args.steps
     achieved = flops_timed / calls / attn_avg_s / 1e12
     # memory-bound pass: qk-norm + RoPE, algorithmic bytes = read + write q and k
     qk_bytes = 2 * (Lv + TXT) * 2 * 2560 * 2
@@ -584,9 +597,12 @@ def main():
                      "traffic": sdpa_bytes, "traffic_unit": "bytes per launch (rocprofv3 PMC)",
                      "kernel": "sdpa_bf16_kernel",
                      "avg_launch_us": round(attn_avg_s * 1e6, 2),
+                     "timing": "HIP events around back-to-back launches of the attention kernel on its "
+                               "stream, per geometry, mixed as in the timed steps (awa_time_attention)",
+                     "frac_by_phase_events": round(flops_timed / calls / attn_evt_s / 1e12 / PEAK_BF16_TFLOPS, 4),
                      "algorithmic_gflop_per_launch": round(flops_timed / calls / 1e9, 3)},
         "phases_us": {"pack_qknorm_rope": round(pack_avg_s * 1e6, 2),
-                      "attention": round(attn_avg_s * 1e6, 2),
+                      "attention": round(attn_evt_s * 1e6, 2),
                       "text_average": round(ms_text * 1e3 / calls, 2)},
         "hbm_qknorm_rope": {"algorithmic_bytes": qk_bytes,
                             "achieved_GBs": round(qk_bytes / pack_avg_s / 1e9, 1),
