@@ -100,12 +100,35 @@ constexpr int VP = 129;
 
 constexpr int RPT = TILE / 16;  // rows per thread (16 rows per 256-thread pass)
 
+// The tile's (cos, sin) table rows staged in LDS: rows cs_row0 .. +63 of the
+// geometry's table are contiguous (64 pairs = 32 float4 per row), so the 256
+// threads read them as one coalesced 32 KiB block, eight float4 each; rows at
+// or past nvalid (padding slots, whose table rows may lie past the table's
+// end) hold the identity rotation.  Each thread then reads its own rows'
+// pairs back from LDS: the 16 lanes of a row read its 512 contiguous bytes.
+constexpr int CS_Q4 = CS_STRIDE / 2;  // float4 per table row
+constexpr int CS_PT = TILE * CS_Q4 / 256;  // float4 per thread
+// The loads are issued before the q/k loads (load_cs) and written to LDS after
+// them (store_cs): the LDS writes then wait only for the table loads.
+__device__ inline void load_cs(float4 (&t)[CS_PT], const float4* cst, size_t cs_row0, int nvalid, int tid) {
+#pragma unroll
+    for (int it = 0; it < CS_PT; it++) {
+        const int i = it * 256 + tid, row = i / CS_Q4;
+        t[it] = row < nvalid ? cst[(cs_row0 + row) * CS_Q4 + (i % CS_Q4)] : make_float4(1.f, 0.f, 1.f, 0.f);
+    }
+}
+__device__ inline void store_cs(float4* lds_cs, const float4 (&t)[CS_PT], int tid) {
+#pragma unroll
+    for (int it = 0; it < CS_PT; it++) lds_cs[it * 256 + tid] = t[it];
+}
+
 // kV: also pack V (fp32 storage).
 template <typename T, bool kV>
 __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     using IO = Io<T>;
     static_assert(!kV || sizeof(T) == 4, "V is packed for fp32 storage only");
     __shared__ uint32_t vs[kV ? TILE * VP : 1];
+    __shared__ float4 lds_cs[TILE * CS_Q4];
 
     const int nblk = a.n_tiles * HEADS;
     const int lid = xcd_remap(nblk);
@@ -134,9 +157,11 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     const float* gk = is_txt ? a.nk_t : a.nk_v;
     const int col = h * HEAD_D + c * 8;
 
-    // Issue every load of the thread: 4 rows x (q, k, [v], 4 cos/sin pairs).
+    // Issue every load of the thread: the tile's (cos, sin) rows for LDS,
+    // then 4 rows x (q, k, [v]).
+    float4 cst_t[CS_PT];
+    load_cs(cst_t, cst, cs_row0, nvalid, tid);
     typename IO::Raw rq[RPT], rk[RPT], rv[RPT];
-    float4 cs[RPT][2];
 #pragma unroll
     for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
@@ -145,13 +170,18 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
             rq[kk] = IO::load(row);
             rk[kk] = IO::load(row + DIM);
             if constexpr (kV) rv[kk] = IO::load(row + 2 * DIM);
-            const float4* p = cst + ((cs_row0 + r) * CS_STRIDE + c * 4) / 2;
-            cs[kk][0] = p[0];
-            cs[kk][1] = p[1];
         } else {
             rq[kk] = rk[kk] = rv[kk] = IO::zero();
-            cs[kk][0] = cs[kk][1] = make_float4(1.f, 0.f, 1.f, 0.f);
         }
+    }
+    store_cs(lds_cs, cst_t, tid);
+    __syncthreads();
+    float4 cs[RPT][2];
+#pragma unroll
+    for (int kk = 0; kk < RPT; kk++) {
+        const int r = r0 + 16 * kk;
+        cs[kk][0] = lds_cs[r * CS_Q4 + 2 * c];
+        cs[kk][1] = lds_cs[r * CS_Q4 + 2 * c + 1];
     }
     float gqv[8], gkv[8];
 #pragma unroll
@@ -226,10 +256,10 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
 
 // bf16 storage: one workgroup per (64-row tile, group of PACK_HG heads).  A
 // thread's row offsets, (cos, sin) pairs and gains are the same for every head
-// of the tile, so the workgroup loads them once and keeps them in registers for
-// its heads (each thread needs only its own rows' pairs: no exchange through
-// LDS); the q and k loads of the next head are in flight while the current
-// head is normalised, rotated and stored.  The output is rounded to bf16, so
+// of the tile, so the workgroup stages the tile's table rows in LDS once
+// (load_cs, store_cs) and each thread keeps its rows' pairs, offsets and gains in
+// registers for its heads; the q and k loads of the next head are in flight
+// while the current head is normalised, rotated and stored.  The output is rounded to bf16, so
 // the arithmetic is the short form: 1/r by v_rsq_f32 (within an ulp of the
 // correctly rounded sqrt and division of the fp32 kernel) and
 // y = ((x g) c -/+ (x' g') s) (1/r [* qscale]), eight operations per channel
@@ -238,6 +268,7 @@ constexpr int PACK_HG = 2;  // heads per workgroup (measured against 1, 4, 5 and
 
 __global__ __launch_bounds__(256) void pack_bf16_kernel(PackArgs a) {
     using IO = Io<uint16_t>;
+    __shared__ float4 lds_cs[TILE * CS_Q4];
     constexpr int NG = HEADS / PACK_HG;
     static_assert(HEADS % PACK_HG == 0, "head groups must tile the heads");
     const int nblk = a.n_tiles * NG;
@@ -276,19 +307,18 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(PackArgs a) {
             }
         }
     };
+    float4 cst_t[CS_PT];
+    load_cs(cst_t, cst, cs_row0, nvalid, tid);
     IO::Raw rq[2][RPT], rk[2][RPT];
     load_head(h0, rq[0], rk[0]);
+    store_cs(lds_cs, cst_t, tid);
+    __syncthreads();
     float4 cs[RPT][2];
 #pragma unroll
     for (int kk = 0; kk < RPT; kk++) {
         const int r = r0 + 16 * kk;
-        if (r < nvalid) {
-            const float4* p = cst + ((cs_row0 + r) * CS_STRIDE + c * 4) / 2;
-            cs[kk][0] = p[0];
-            cs[kk][1] = p[1];
-        } else {
-            cs[kk][0] = cs[kk][1] = make_float4(1.f, 0.f, 1.f, 0.f);
-        }
+        cs[kk][0] = lds_cs[r * CS_Q4 + 2 * c];
+        cs[kk][1] = lds_cs[r * CS_Q4 + 2 * c + 1];
     }
     float gqv[8], gkv[8];
 #pragma unroll

@@ -35,27 +35,34 @@ __global__ __launch_bounds__(256) void norm_ada_kernel(NormArgs a) {
     float4 v[PER_LANE4];
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < PER_LANE4; i++) {
-        v[i] = x[i * 64 + lane];
-        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    }
-    ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / (float)DIM + a.eps);
+    for (int i = 0; i < PER_LANE4; i++) v[i] = x[i * 64 + lane];
+    // the modulation vectors (cached, the same for every row) are loaded
+    // while the row is in flight, not after the reduction
     const bool second = row >= a.split;
     const float* sc = second ? a.scale1 : a.scale0;
     const float* sh = second ? a.shift1 : a.shift0;
+    float4 s[PER_LANE4], t[PER_LANE4];
+    if (sc) {
+#pragma unroll
+        for (int i = 0; i < PER_LANE4; i++) {
+            s[i] = reinterpret_cast<const float4*>(sc)[i * 64 + lane];
+            t[i] = reinterpret_cast<const float4*>(sh)[i * 64 + lane];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PER_LANE4; i++)
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)DIM + a.eps);
     uint2* out = reinterpret_cast<uint2*>(a.h + (size_t)row * DIM);
 #pragma unroll
     for (int i = 0; i < PER_LANE4; i++) {
-        const int c = (i * 64 + lane) * 4;
         float o0 = v[i].x * r, o1 = v[i].y * r, o2 = v[i].z * r, o3 = v[i].w * r;
         if (sc) {
-            const float4 s = *reinterpret_cast<const float4*>(sc + c);
-            const float4 t = *reinterpret_cast<const float4*>(sh + c);
-            o0 = o0 * s.x + t.x;
-            o1 = o1 * s.y + t.y;
-            o2 = o2 * s.z + t.z;
-            o3 = o3 * s.w + t.w;
+            o0 = o0 * s[i].x + t[i].x;
+            o1 = o1 * s[i].y + t[i].y;
+            o2 = o2 * s[i].z + t[i].z;
+            o3 = o3 * s[i].w + t[i].w;
         }
         out[i * 64 + lane] = make_uint2(bf16x2_rne(o0, o1), bf16x2_rne(o2, o3));
     }
