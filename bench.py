@@ -141,22 +141,25 @@ def config_runs(ctx, torch, steps, cpu=True):
         es = 4 if store == "f32" else 2
         peak = PEAK_FP32_TFLOPS if store == "f32" else PEAK_BF16_TFLOPS
         attn_s = ma * 1e-3 / c
-        # the kernel's own time: back-to-back launches between two events
-        attn_k = ctx.time_attention(g, vq, tq, *gains, reps=max(4, steps), eps=1e-5, vattn=va, tattn=ta) * 1e-3
+        # the kernels' own times: back-to-back launches between two events
+        pk_k, attn_k, tx_k = (x * 1e-3 for x in ctx.time_phases(g, vq, tq, *gains, reps=max(4, steps), eps=1e-5,
+                                                                  vattn=va, tattn=ta))
         tfl = fl / attn_k / 1e12
         qk_bytes = 2 * (Lv + txt) * 2 * 2560 * es
         co_bytes = (g.info()["nwin"] + 1) * txt * 2560 * 4
         r = {"grid": list(grid), "num_windows": list(nw), "txt_len": txt, "shifted": bool(sh),
              "storage": store, "nwin": g.info()["nwin"], "ms_per_layer": round(layer_ms, 4),
-             "phases_us": {"pack": round(mp * 1e3 / c, 2), "attention": round(attn_s * 1e6, 2),
-                           "text_average": round(mt * 1e3 / c, 2)},
+             "phases_us": {"pack": round(pk_k * 1e6, 2), "attention": round(attn_k * 1e6, 2),
+                           "text_average": round(tx_k * 1e6, 2)},
+             "phases_us_by_events": {"pack": round(mp * 1e3 / c, 2), "attention": round(attn_s * 1e6, 2),
+                                     "text_average": round(mt * 1e3 / c, 2)},
              "attention_roofline": {"bound": "mfma", "achieved": round(tfl, 1), "peak": peak,
                                     "unit": "TFLOP/s", "frac": round(tfl / peak, 4),
                                     "avg_launch_us": round(attn_k * 1e6, 2),
                                     "frac_by_phase_events": round(fl / attn_s / 1e12 / peak, 4),
                                     "gflop_per_launch": round(fl / 1e9, 3)},
-             "hbm_qknorm_rope_frac": round(qk_bytes / (mp * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4),
-             "hbm_text_average_frac": round(co_bytes / (mt * 1e-3 / c) / 1e9 / PEAK_HBM_GBS, 4)}
+             "hbm_qknorm_rope_frac": round(qk_bytes / pk_k / 1e9 / PEAK_HBM_GBS, 4),
+             "hbm_text_average_frac": round(co_bytes / tx_k / 1e9 / PEAK_HBM_GBS, 4)}
         if cpu:
             sys.path.insert(0, os.path.join(ROOT, "oracle"))
             import oracle as O
@@ -552,17 +555,18 @@ def main():
     n_sh = args.steps // 2
     flops_timed = n_unsh * flops[0] + n_sh * flops[1]
     attn_evt_s = ms_attn * 1e-3 / calls  # per-phase events: the launch gap after each event included
-    # the kernel's own time: HIP events around `steps` back-to-back launches of
-    # the attention kernel per geometry on its stream (awa_time_attention), the
-    # timed mix of the two geometries
+    # the kernels' own times: HIP events around `steps` back-to-back launches of
+    # each kernel per geometry on its stream (awa_time_phases), the timed mix of
+    # the two geometries
     reps = max(4, args.steps)
-    t_attn = [ctx.time_attention(geoms[k], vq, tq, *gains, reps=reps, eps=1e-5, vattn=vattn, tattn=tattn) * 1e-3
-              for k in range(2)]
-    attn_avg_s = (n_unsh * t_attn[0] + n_sh * t_attn[1]) / args.steps
+    t_ph = [ctx.time_phases(geoms[k], vq, tq, *gains, reps=reps, eps=1e-5, vattn=vattn, tattn=tattn)
+            for k in range(2)]
+    mix = lambda i: (n_unsh * t_ph[0][i] + n_sh * t_ph[1][i]) * 1e-3 / args.steps
+    attn_avg_s = mix(1)
     achieved = flops_timed / calls / attn_avg_s / 1e12
     # memory-bound pass: qk-norm + RoPE, algorithmic bytes = read + write q and k
     qk_bytes = 2 * (Lv + TXT) * 2 * 2560 * 2
-    pack_avg_s = ms_pack * 1e-3 / calls
+    pack_avg_s = mix(0)
     traffic = measured_traffic()
     sdpa_bytes = traffic.get("sdpa_bf16_kernel", {}).get("total_bytes")
     pack_bytes = traffic.get("pack_bf16_kernel", {}).get("total_bytes")
@@ -598,12 +602,17 @@ def main():
                      "kernel": "sdpa_bf16_kernel",
                      "avg_launch_us": round(attn_avg_s * 1e6, 2),
                      "timing": "HIP events around back-to-back launches of the attention kernel on its "
-                               "stream, per geometry, mixed as in the timed steps (awa_time_attention)",
+                               "stream, per geometry, mixed as in the timed steps (awa_time_phases)",
                      "frac_by_phase_events": round(flops_timed / calls / attn_evt_s / 1e12 / PEAK_BF16_TFLOPS, 4),
                      "algorithmic_gflop_per_launch": round(flops_timed / calls / 1e9, 3)},
         "phases_us": {"pack_qknorm_rope": round(pack_avg_s * 1e6, 2),
-                      "attention": round(attn_evt_s * 1e6, 2),
-                      "text_average": round(ms_text * 1e3 / calls, 2)},
+                      "attention": round(attn_avg_s * 1e6, 2),
+                      "text_average": round(mix(2) * 1e6, 2),
+                      "timing": "each kernel back to back between two events (awa_time_phases)"},
+        "phases_us_by_events": {"pack_qknorm_rope": round(ms_pack * 1e3 / calls, 2),
+                                "attention": round(attn_evt_s * 1e6, 2),
+                                "text_average": round(ms_text * 1e3 / calls, 2),
+                                "timing": "per-phase events of the timed eager steps (launch gaps included)"},
         "hbm_qknorm_rope": {"algorithmic_bytes": qk_bytes,
                             "achieved_GBs": round(qk_bytes / pack_avg_s / 1e9, 1),
                             "frac": round(qk_bytes / pack_avg_s / 1e9 / PEAK_HBM_GBS, 4),
@@ -617,12 +626,15 @@ def main():
     out["hbm_qknorm_rope"]["frac_of_copy"] = round(qk_bytes / pack_avg_s / 1e9 / ceil["GBs"], 4)
     # the text average against HBM: (nwin + 1) TXT 2560 fp32 bytes per launch
     co_bytes = [(infos[k]["nwin"] + 1) * TXT * 2560 * 4 for k in range(2)]
-    text_avg_s = ms_text * 1e-3 / calls
-    out["hbm_text_average"] = {"algorithmic_bytes": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls),
-                               "achieved_GBs": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls
-                                                     / text_avg_s / 1e9, 1),
-                               "frac": round((n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls
-                                             / text_avg_s / 1e9 / PEAK_HBM_GBS, 4)}
+    text_avg_s = mix(2)
+    co_mix = (n_unsh * co_bytes[0] + n_sh * co_bytes[1]) / calls
+    out["hbm_text_average"] = {"algorithmic_bytes": round(co_mix),
+                               "achieved_GBs": round(co_mix / text_avg_s / 1e9, 1),
+                               "frac": round(co_mix / text_avg_s / 1e9 / PEAK_HBM_GBS, 4),
+                               "note": "back-to-back repeats re-read the partials from the L2 caches (an upper "
+                                       "bound); inside the layer they come from the attention kernel's writes",
+                               "frac_by_phase_events": round(co_mix / (ms_text * 1e-3 / calls) / 1e9
+                                                             / PEAK_HBM_GBS, 4)}
     if not args.no_configs:
         out["configs"] = config_runs(ctx, torch, max(4, args.steps // 2), cpu=not args.no_cpu_baseline)
     if not args.no_dit:

@@ -169,16 +169,17 @@ int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv,
  * awa_timing_read waits for the recorded events, returns the summed
  * milliseconds of each phase and the number of calls, and clears them. */
 int awa_timing_enable(awa_ctx* ctx, int enable);
-/* awa_forward, then its attention kernel launched `reps` more times back to
- * back on `stream` between two events (same inputs, same outputs);
- * *ms_per_launch receives the mean per launch and the call returns after the
- * last one.  No counterpart in the reference: it times the attention kernel
- * without the per-phase events of awa_timing_enable between launches (for the
- * roofline figure of bench.py). */
-int awa_time_attention(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
-                       int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
-                       const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, int reps,
-                       double* ms_per_launch, awa_stream_t stream);
+/* awa_forward, then each of its three kernels (pack, attention, text
+ * average) launched `reps` more times back to back on `stream` between two
+ * events (same inputs, same outputs); ms_per_launch[0..2] receive the mean
+ * per launch of each and the call returns after the last one.  No
+ * counterpart in the reference: it times the kernels without the per-phase
+ * events of awa_timing_enable between launches (the roofline figures of
+ * bench.py). */
+int awa_time_phases(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
+                    int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
+                    const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, int reps,
+                    double ms_per_launch[3], awa_stream_t stream);
 int awa_timing_read(awa_ctx* ctx, double* ms_pack, double* ms_attn, double* ms_text, int* calls);
 
 /* Casts at the bf16 boundary (cast_f32_bf16.comp:23-24, round to nearest

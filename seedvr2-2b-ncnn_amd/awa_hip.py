@@ -144,8 +144,8 @@ def lib():
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_stream_copy.argtypes = [vp, vp, vp, C.c_int64, vp]
-        L.awa_time_attention.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
-                                         C.c_float, vp, vp, C.c_int, C.POINTER(C.c_double), vp]
+        L.awa_time_phases.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
+                                      C.c_float, vp, vp, C.c_int, C.POINTER(C.c_double), vp]
         _lib = L
     return _lib
 
@@ -363,10 +363,11 @@ class Context:
         self._keep = gains  # alive until the stream consumed them
         return vattn, tattn
 
-    def time_attention(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, reps, eps=1e-5, vattn=None,
-                       tattn=None, stream=None):
-        """awa_time_attention: the op, then its attention kernel `reps` more times
-        back to back between two events; returns the mean ms per launch."""
+    def time_phases(self, geom, vqkv, tqkv, nq_v, nk_v, nq_t, nk_t, reps, eps=1e-5, vattn=None,
+                    tattn=None, stream=None):
+        """awa_time_phases: the op, then each of its kernels (pack, attention,
+        text average) `reps` more times back to back between two events;
+        returns the mean ms per launch of each, (pack, attention, text)."""
         import torch
         dtype = AWA_BF16 if vqkv.dtype == torch.bfloat16 else AWA_F32
         Lv, TXT = vqkv.shape[0], tqkv.shape[0]
@@ -375,14 +376,14 @@ class Context:
             vattn = torch.empty((Lv, DIM), dtype=vqkv.dtype, device=vqkv.device)
         if tattn is None:
             tattn = torch.empty((TXT, DIM), dtype=vqkv.dtype, device=vqkv.device)
-        ms = C.c_double(0.0)
-        rc = lib().awa_time_attention(self.ptr, geom.ptr, dtype, C.c_void_p(vqkv.data_ptr()),
-                                      C.c_void_p(tqkv.data_ptr()), Lv, TXT,
-                                      *[C.c_void_p(g.data_ptr()) for g in gains], float(eps),
-                                      C.c_void_p(vattn.data_ptr()), C.c_void_p(tattn.data_ptr()), int(reps),
-                                      C.byref(ms), _stream_ptr(stream))
-        self.check(rc, "awa_time_attention")
-        return ms.value
+        ms = (C.c_double * 3)()
+        rc = lib().awa_time_phases(self.ptr, geom.ptr, dtype, C.c_void_p(vqkv.data_ptr()),
+                                   C.c_void_p(tqkv.data_ptr()), Lv, TXT,
+                                   *[C.c_void_p(g.data_ptr()) for g in gains], float(eps),
+                                   C.c_void_p(vattn.data_ptr()), C.c_void_p(tattn.data_ptr()), int(reps),
+                                   ms, _stream_ptr(stream))
+        self.check(rc, "awa_time_phases")
+        return ms[0], ms[1], ms[2]
 
     # ---- boundary casts
     def cast_f32_to_bf16(self, src, out, stream=None):

@@ -397,8 +397,8 @@ size_t op_scratch_bytes(const GeomPlan& P, int dtype) {
 
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
-                 float eps, void* d_vattn, void* d_tattn, hipStream_t s, void* ext_scratch, int attn_reps,
-                 double* attn_ms) {
+                 float eps, void* d_vattn, void* d_tattn, hipStream_t s, void* ext_scratch, int reps,
+                 double* phase_ms) {
     const GeomPlan& P = g->plan;
     const int Lv = P.Lv;
     const size_t es = elem_size(dtype);
@@ -455,20 +455,25 @@ int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv,
 
     HIPCK(ctx, launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s));
     HIPCK(ctx, mark());
-    if (attn_reps > 0 && attn_ms) {
+    if (reps > 0 && phase_ms) {
         hipEvent_t e[2] = {nullptr, nullptr};
         hipError_t r = hipEventCreate(&e[0]);
         if (r == hipSuccess) r = hipEventCreate(&e[1]);
-        if (r == hipSuccess) r = hipEventRecord(e[0], s);
-        for (int i = 0; i < attn_reps && r == hipSuccess; i++) r = launch_sdpa(dtype, sa, s);
-        if (r == hipSuccess) r = hipEventRecord(e[1], s);
-        if (r == hipSuccess) r = hipEventSynchronize(e[1]);
-        float ms = 0.f;
-        if (r == hipSuccess) r = hipEventElapsedTime(&ms, e[0], e[1]);
+        for (int ph = 0; ph < 3 && r == hipSuccess; ph++) {
+            r = hipEventRecord(e[0], s);
+            for (int i = 0; i < reps && r == hipSuccess; i++)
+                r = ph == 0 ? launch_pack(dtype, pa, s)
+                  : ph == 1 ? launch_sdpa(dtype, sa, s)
+                            : launch_coalesce(dtype, sa.tpart, d_tattn, P.nwin, P.txt_len, s);
+            if (r == hipSuccess) r = hipEventRecord(e[1], s);
+            if (r == hipSuccess) r = hipEventSynchronize(e[1]);
+            float ms = 0.f;
+            if (r == hipSuccess) r = hipEventElapsedTime(&ms, e[0], e[1]);
+            phase_ms[ph] = (double)ms / reps;
+        }
         for (hipEvent_t x : e)
             if (x) (void)hipEventDestroy(x);
         HIPCK(ctx, r);
-        *attn_ms = (double)ms / attn_reps;
     }
     return AWA_OK;
 }
@@ -925,15 +930,15 @@ int awa_forward_host(awa_ctx* ctx, const awa_geom* g, const float* h_vqkv, const
     return rc;
 }
 
-int awa_time_attention(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
-                       int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
-                       const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, int reps,
-                       double* ms_per_launch, awa_stream_t stream) {
-    const int rc = check_forward_args("awa_time_attention", ctx, g, dtype, d_vqkv, d_tqkv, Lv, TXT, d_nq_v,
+int awa_time_phases(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
+                    int Lv, int TXT, const float* d_nq_v, const float* d_nk_v, const float* d_nq_t,
+                    const float* d_nk_t, float eps, void* d_vattn, void* d_tattn, int reps,
+                    double ms_per_launch[3], awa_stream_t stream) {
+    const int rc = check_forward_args("awa_time_phases", ctx, g, dtype, d_vqkv, d_tqkv, Lv, TXT, d_nq_v,
                                       d_nk_v, d_nq_t, d_nk_t, eps, d_vattn, d_tattn);
     if (rc != AWA_OK) return rc;
     if (reps < 1 || !ms_per_launch) {
-        set_err(ctx, "awa_time_attention: reps=%d must be positive and ms_per_launch non-null", reps);
+        set_err(ctx, "awa_time_phases: reps=%d must be positive and ms_per_launch non-null", reps);
         return AWA_EARG;
     }
     DeviceGuard dg(ctx->device);

@@ -238,13 +238,14 @@ size_t op_scratch_bytes(const GeomPlan& P, int dtype);
 // nullptr uses the context's scratch (grown on demand, per-phase events when
 // timing is on); otherwise a caller-provided device buffer of at least
 // op_scratch_bytes, and nothing is allocated or recorded.
-// attn_reps > 0 (with attn_ms): after the op, the attention kernel is launched
-// attn_reps more times back to back between two events (the same inputs, so
-// the same outputs) and *attn_ms receives the mean time per launch.
+// reps > 0 (with phase_ms[3]): after the op, each of its three kernels (pack,
+// attention, text average) is launched reps more times back to back between
+// two events (the same inputs, so the same outputs), and phase_ms receives
+// the mean time per launch of each.
 int forward_impl(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vqkv, const void* d_tqkv,
                  const float* d_nq_v, const float* d_nk_v, const float* d_nq_t, const float* d_nk_t,
                  float eps, void* d_vattn, void* d_tattn, hipStream_t s, void* ext_scratch = nullptr,
-                 int attn_reps = 0, double* attn_ms = nullptr);
+                 int reps = 0, double* phase_ms = nullptr);
 // The allocation-free entry's per-device scratch (awa_noalloc.hip):
 // noalloc_resolve looks up the device address of the current device's copy
 // (call with that device current); noalloc_scratch returns it, or nullptr.
