@@ -1,9 +1,9 @@
 // awa_pack.hip — fused qk RMSNorm + 3-D RoPE + window partition.
 //
-// One workgroup per (64-row tile, head) for fp32 storage, per (tile, two
-// heads) for bf16; the workgroups of a tile are neighbouring work indices on
-// one XCD, so the tile's (cos, sin) rows come from HBM once and from that
-// XCD's L2 for the other heads.  It gathers the
+// One workgroup per (16-row quarter of a 64-row tile, head) for fp32
+// storage, per (tile, two heads) for bf16; the workgroups of a tile are
+// neighbouring work indices on one XCD, so the tile's (cos, sin) rows come
+// from HBM once and from that XCD's L2 for the other heads, staged in LDS.  It gathers the
 // tile's rows from vqkv / tqkv (window order of vidx, awa_vk.cpp:73-88, through
 // the geometry's row table),
 // normalises q and k per head (dit_vk.cpp:54-61: r = sqrt(sum x^2 / 128 +
@@ -98,7 +98,7 @@ __device__ inline float div_by(float x, float r, float rinv) {
 // both hit distinct banks.
 constexpr int VP = 129;
 
-constexpr int RPT = TILE / 16;  // rows per thread (16 rows per 256-thread pass)
+constexpr int RPT = TILE / 16;  // rows per thread of the bf16 kernel (16 rows per 256-thread pass)
 
 // The tile's (cos, sin) table rows staged in LDS: rows cs_row0 .. +63 of the
 // geometry's table are contiguous (64 pairs = 32 float4 per row), so the 256
@@ -122,66 +122,72 @@ __device__ inline void store_cs(float4* lds_cs, const float4 (&t)[CS_PT], int ti
     for (int it = 0; it < CS_PT; it++) lds_cs[it * 256 + tid] = t[it];
 }
 
-// kV: also pack V (fp32 storage).
-template <typename T, bool kV>
-__global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
-    using IO = Io<T>;
-    static_assert(!kV || sizeof(T) == 4, "V is packed for fp32 storage only");
-    __shared__ uint32_t vs[kV ? TILE * VP : 1];
-    __shared__ float4 lds_cs[TILE * CS_Q4];
+// fp32 storage: one workgroup per (QR rows of a 64-row tile, head), QR / 16
+// rows per thread (16 threads per row, each an 8-channel chunk).  QR = 64
+// (whole tiles) when the grid fills the device; QR = 16 (four workgroups per
+// tile and head) for small geometries, whose whole-tile grid has fewer
+// workgroups than the device has CUs (220 at 360p).  Correctly rounded
+// arithmetic (IEEE sqrt, division by div_by); V is packed transposed through
+// LDS: the workgroup's QR slots of every channel row of the V^T tile.
+// whole-tile workgroups from this many (tile, head) pairs on (measured: quarters
+// faster up to 1,200 pairs (360p 12.0 -> 10.2 us, 720p 31 -> 26), whole tiles
+// from 1,900 (1080p 79 against 86 us))
+constexpr long F32_WHOLE_MIN = 1536;
+template <int QR>
+__global__ __launch_bounds__(256) void pack_f32_kernel(PackArgs a) {
+    using IO = Io<float>;
+    constexpr int NQ = TILE / QR;                 // workgroups per (tile, head)
+    constexpr int RT = QR / 16;                   // rows per thread
+    constexpr int NCS = QR * CS_Q4 / 256;         // table float4 per thread
+    __shared__ uint32_t vs[QR * VP];
+    __shared__ float4 lds_cs[QR * CS_Q4];
 
-    const int nblk = a.n_tiles * HEADS;
-    const int lid = xcd_remap(nblk);
+    const int nblk = a.n_tiles * HEADS * NQ;
+    const int lid = xcd_remap(nblk);  // a tile's workgroups: neighbouring ids, one XCD
     if (lid >= nblk) return;
-    const int tile = lid / HEADS;
-    const int h = lid - tile * HEADS;
+    const int tile = lid / (HEADS * NQ);
+    const int rem = lid - tile * (HEADS * NQ);
+    const int h = rem / NQ, qt = rem - (rem / NQ) * NQ;
     const int tid = threadIdx.x;
-    const int c = tid & 15;     // 8-channel chunk of the head row
-    const int r0 = tid >> 4;    // first slot handled by this thread
+    const int c = tid & 15;                  // 8-channel chunk of the head row
+    const int rl = tid >> 4;                 // first row of the thread in the workgroup
 
     // Two levels of loads: the tile's record (RoPE-table row of slot 0,
-    // valid rows) and the thread's row indices from the row table (entries
-    // exist for all 64 rows), then every data load of the thread.
+    // valid rows) and the thread's row indices from the row table, then every
+    // data load of the thread.
     const bool is_txt = tile >= a.n_vid_tiles;
     const int2 meta = reinterpret_cast<const int2*>(a.tile_meta)[tile];
     const uint32_t* rows =
         a.vrow + (size_t)(is_txt ? a.n_vid_tiles + (tile - a.n_vid_tiles) % a.ntt : tile) * TILE;
-    uint32_t ridx[RPT];
+    uint32_t ridx[RT];
 #pragma unroll
-    for (int kk = 0; kk < RPT; kk++) ridx[kk] = rows[vrow_pos(r0 + 16 * kk)];
+    for (int kk = 0; kk < RT; kk++) ridx[kk] = rows[vrow_pos(qt * QR + rl + 16 * kk)];
     const int nvalid = meta.y;
     const size_t cs_row0 = (size_t)meta.x;  // table row of slot 0
-    const T* src = reinterpret_cast<const T*>(is_txt ? a.tqkv : a.vqkv);
+    const float* src = reinterpret_cast<const float*>(is_txt ? a.tqkv : a.vqkv);
     const float4* cst = reinterpret_cast<const float4*>(is_txt ? a.tcs : a.vcs);
     const float* gq = is_txt ? a.nq_t : a.nq_v;
     const float* gk = is_txt ? a.nk_t : a.nk_v;
     const int col = h * HEAD_D + c * 8;
 
-    // Issue every load of the thread: the tile's (cos, sin) rows for LDS,
-    // then 4 rows x (q, k, [v]).
-    float4 cst_t[CS_PT];
-    load_cs(cst_t, cst, cs_row0, nvalid, tid);
-    typename IO::Raw rq[RPT], rk[RPT], rv[RPT];
+    // the workgroup's (cos, sin) rows for LDS, then the rows' q, k, v
+    float4 cst_t[NCS];
 #pragma unroll
-    for (int kk = 0; kk < RPT; kk++) {
-        const int r = r0 + 16 * kk;
-        if (r < nvalid) {  // uniform across the 16 lanes of a row
-            const T* row = src + (size_t)ridx[kk] + col;
+    for (int it = 0; it < NCS; it++) {
+        const int i = it * 256 + tid, row = qt * QR + i / CS_Q4;
+        cst_t[it] = row < nvalid ? cst[(cs_row0 + row) * CS_Q4 + (i % CS_Q4)] : make_float4(1.f, 0.f, 1.f, 0.f);
+    }
+    IO::Raw rq[RT], rk[RT], rv[RT];
+#pragma unroll
+    for (int kk = 0; kk < RT; kk++) {
+        if (qt * QR + rl + 16 * kk < nvalid) {  // uniform across the 16 lanes of a row
+            const float* row = src + (size_t)ridx[kk] + col;
             rq[kk] = IO::load(row);
             rk[kk] = IO::load(row + DIM);
-            if constexpr (kV) rv[kk] = IO::load(row + 2 * DIM);
+            rv[kk] = IO::load(row + 2 * DIM);
         } else {
             rq[kk] = rk[kk] = rv[kk] = IO::zero();
         }
-    }
-    store_cs(lds_cs, cst_t, tid);
-    __syncthreads();
-    float4 cs[RPT][2];
-#pragma unroll
-    for (int kk = 0; kk < RPT; kk++) {
-        const int r = r0 + 16 * kk;
-        cs[kk][0] = lds_cs[r * CS_Q4 + 2 * c];
-        cs[kk][1] = lds_cs[r * CS_Q4 + 2 * c + 1];
     }
     float gqv[8], gkv[8];
 #pragma unroll
@@ -189,15 +195,20 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         gqv[i] = gq[c * 8 + i];
         gkv[i] = gk[c * 8 + i];
     }
+#pragma unroll
+    for (int it = 0; it < NCS; it++) lds_cs[it * 256 + tid] = cst_t[it];
+    __syncthreads();
 
     const size_t tile_off = ((size_t)h * a.n_tiles + tile) * TILE * HEAD_D;
-    T* Qt = reinterpret_cast<T*>(a.Qp) + tile_off;
-    T* Kt = reinterpret_cast<T*>(a.Kp) + tile_off;
-    T* Vt = kV ? reinterpret_cast<T*>(a.Vp) + tile_off : nullptr;
+    float* Qt = reinterpret_cast<float*>(a.Qp) + tile_off;
+    float* Kt = reinterpret_cast<float*>(a.Kp) + tile_off;
+    float* Vt = reinterpret_cast<float*>(a.Vp) + tile_off;
 
 #pragma unroll
-    for (int kk = 0; kk < RPT; kk++) {
-        const int r = r0 + 16 * kk;
+    for (int kk = 0; kk < RT; kk++) {
+        const int lr = rl + 16 * kk;       // row in the workgroup
+        const int r = qt * QR + lr;        // slot in the tile
+        const float4 cs0 = lds_cs[lr * CS_Q4 + 2 * c], cs1 = lds_cs[lr * CS_Q4 + 2 * c + 1];
         float q[8], k[8];
         IO::widen(rq[kk], q);
         IO::widen(rk[kk], k);
@@ -212,8 +223,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         const float nq = sqrtf(sq / (float)HEAD_D + a.eps);
         const float nk = sqrtf(sk / (float)HEAD_D + a.eps);
         const float iq = 1.f / nq, ik = 1.f / nk;
-        const float csv[8] = {cs[kk][0].x, cs[kk][0].y, cs[kk][0].z, cs[kk][0].w,
-                              cs[kk][1].x, cs[kk][1].y, cs[kk][1].z, cs[kk][1].w};
+        const float csv[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const float cn = csv[2 * p], sn = csv[2 * p + 1];
@@ -228,29 +238,27 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
         }
         IO::store8(Qt + (size_t)r * HEAD_D + c * 8, q);
         IO::store8(Kt + (size_t)r * HEAD_D + c * 8, k);
-        if constexpr (kV) {
-            float v[8];
-            IO::widen(rv[kk], v);
-            uint32_t* vrow = vs + r * VP;
+        float v[8];
+        IO::widen(rv[kk], v);
+        uint32_t* vrow = vs + lr * VP;
 #pragma unroll
-            for (int i = 0; i < 8; i++) vrow[c * 8 + i] = __float_as_uint(v[i]);
-        }
+        for (int i = 0; i < 8; i++) vrow[c * 8 + i] = __float_as_uint(v[i]);
     }
-    if constexpr (!kV) return;
     __syncthreads();
 
-    // Transposed V tile Vt[d][slot] (fp32), written as whole 256-byte rows by
-    // consecutive lanes: thread unit (d, 4-slot chunk sc), 16 chunks per row.
+    // Transposed V: Vt[d][slot] for the workgroup's QR slots, 4 QR contiguous
+    // bytes per channel row (thread unit: channel d, 4-slot chunk sc).
+    constexpr int NSC = QR / 4;
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
+    for (int it = 0; it < QR * HEAD_D / 4 / 256; it++) {
         const int u = it * 256 + tid;
-        const int d = u >> 4, sc = u & 15;
+        const int d = u / NSC, sc = u % NSC;
         float4 o;
         o.x = __uint_as_float(vs[(sc * 4 + 0) * VP + d]);
         o.y = __uint_as_float(vs[(sc * 4 + 1) * VP + d]);
         o.z = __uint_as_float(vs[(sc * 4 + 2) * VP + d]);
         o.w = __uint_as_float(vs[(sc * 4 + 3) * VP + d]);
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(Vt) + (size_t)d * TILE + sc * 4) = o;
+        *reinterpret_cast<float4*>(Vt + (size_t)d * TILE + qt * QR + sc * 4) = o;
     }
 }
 
@@ -377,8 +385,11 @@ hipError_t launch_pack(int dtype, const PackArgs& a, hipStream_t s) {
     const dim3 block(256);
     if (dtype == AWA_BF16)
         hipLaunchKernelGGL(pack_bf16_kernel, dim3(xcd_grid((long)a.n_tiles * (HEADS / PACK_HG))), block, 0, s, a);
+    else if ((long)a.n_tiles * HEADS >= F32_WHOLE_MIN)
+        hipLaunchKernelGGL(pack_f32_kernel<TILE>, dim3(xcd_grid((long)a.n_tiles * HEADS)), block, 0, s, a);
     else
-        hipLaunchKernelGGL((pack_kernel<float, true>), dim3(xcd_grid((long)a.n_tiles * HEADS)), block, 0, s, a);
+        hipLaunchKernelGGL(pack_f32_kernel<16>, dim3(xcd_grid((long)a.n_tiles * HEADS * (TILE / 16))), block, 0, s,
+                           a);
     return hipGetLastError();
 }
 
