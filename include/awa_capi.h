@@ -124,6 +124,13 @@ int awa_geom_read(awa_ctx* ctx, const awa_geom* g, int32_t* h_slices, int32_t* h
 
 void awa_geom_destroy(awa_geom* g);
 
+/* Sizes the context's scratch for awa_forward on geometry g in storage dtype,
+ * so that a later call at that geometry allocates nothing (a caller capturing
+ * awa_forward into a graph; awa_geom_build already reserves the bf16 size).
+ * No counterpart in the reference: AwaLayer allocates its buffers in
+ * create_pipeline (awa_layer.cpp:143-255), for one fixed shape. */
+int awa_reserve(awa_ctx* ctx, const awa_geom* g, int dtype);
+
 /* The AWA op, AwaLayer::forward (awa_layer.cpp:284-453): per-head qk RMSNorm
  * (gains shared across heads, eps), 3-D RoPE on 126 channels, window SDPA
  * with the text rows appended to every window, text outputs averaged over the

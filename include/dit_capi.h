@@ -76,11 +76,19 @@ int dit_time_embedding(awa_ctx* ctx, float t, const float* d_w_in, const float* 
  * d_emb is the timestep embedding [15360].  mlp is the SwiGLU width (6912 in
  * the reference checkpoint).  Scratch comes from the context: its workspace
  * grows (hipMalloc) on the first call with a larger shape, so a caller that
- * captures this call into a graph runs it once eagerly at that shape first
- * (dit_graph_create does). */
+ * captures this call into a graph calls dit_reserve at that shape first (or
+ * runs it once eagerly, as dit_graph_create does). */
 int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb,
                       const dit_branch* tb, const float* d_emb, int mlp, int txt_vid_only,
                       float eps, float* d_x, int Lv, int TXT, awa_stream_t stream);
+
+/* Sizes the context's workspace and the AWA scratch for dit_layer_forward,
+ * dit_embed and dit_final on geometry g (Lv video rows, TXT text rows) and
+ * MLP width mlp, so that those calls at that shape allocate nothing: a caller
+ * may then capture them into a graph without an eager run first.  No
+ * counterpart in the reference (DitVk::init sizes its buffers per resolution,
+ * dit_vk.cpp:140-203). */
+int dit_reserve(awa_ctx* ctx, const awa_geom* g, int mlp);
 
 /* Per-phase device timing of dit_layer_forward (HIP events on its stream):
  * GEMMs, AWA op, and norms/elementwise, summed since the last read. */

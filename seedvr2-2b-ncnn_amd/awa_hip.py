@@ -144,6 +144,8 @@ def lib():
         L.awa_cast_f32_to_bf16.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_cast_bf16_to_f32.argtypes = [vp, vp, vp, C.c_int64, vp]
         L.awa_stream_copy.argtypes = [vp, vp, vp, C.c_int64, vp]
+        L.awa_reserve.argtypes = [vp, vp, C.c_int]
+        L.dit_reserve.argtypes = [vp, vp, C.c_int]
         L.awa_time_phases.argtypes = [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, vp, vp,
                                       C.c_float, vp, vp, C.c_int, C.POINTER(C.c_double), vp]
         _lib = L
@@ -444,6 +446,14 @@ class Context:
                                       C.c_void_p(emb.data_ptr()), _stream_ptr(stream))
         self.check(rc, "dit_time_embedding")
         return emb
+
+    def reserve(self, geom, dtype="bf16"):
+        """awa_reserve: size the op's scratch for geom in this storage dtype."""
+        self.check(lib().awa_reserve(self.ptr, geom.ptr, AWA_BF16 if dtype == "bf16" else AWA_F32), "awa_reserve")
+
+    def dit_reserve(self, geom, mlp=6912):
+        """dit_reserve: size the layer / embed / final workspaces and the op's scratch."""
+        self.check(lib().dit_reserve(self.ptr, geom.ptr, int(mlp)), "dit_reserve")
 
     def layer(self, geom, vbranch, tbranch, emb, x, Lv, TXT, mlp=6912, txt_vid_only=False, eps=1e-5,
               stream=None):

@@ -946,6 +946,19 @@ int awa_time_phases(awa_ctx* ctx, const awa_geom* g, int dtype, const void* d_vq
                         reinterpret_cast<hipStream_t>(stream), nullptr, reps, ms_per_launch);
 }
 
+int awa_reserve(awa_ctx* ctx, const awa_geom* g, int dtype) {
+    if (!ctx || !g || (dtype != AWA_F32 && dtype != AWA_BF16)) {
+        set_err(ctx, "awa_reserve: bad argument");
+        return AWA_EARG;
+    }
+    if (g->device != ctx->device) {
+        set_err(ctx, "awa_reserve: geometry of device %d, context of device %d", g->device, ctx->device);
+        return AWA_EARG;
+    }
+    DeviceGuard dg(ctx->device);
+    return ensure_scratch(ctx, op_scratch_bytes(g->plan, dtype));
+}
+
 int awa_timing_enable(awa_ctx* ctx, int enable) {
     if (!ctx) return AWA_EARG;
     ctx->timing = enable != 0;

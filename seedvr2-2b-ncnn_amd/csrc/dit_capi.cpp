@@ -1,6 +1,7 @@
 // dit_capi.cpp — C ABI of the DiT block: one layer of DitVk::forward_latent
 // (dit_vk.cpp:517-632) as norm -> GEMM -> AWA -> GEMM -> norm -> GEMM -> GEMM
 // on the caller's stream.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -99,6 +100,32 @@ void dit_io_destroy(awa_ctx* ctx, dit_io* io) {
     delete io;
 }
 
+namespace {
+// workspace bytes of each entry point (the offsets below follow the same layouts)
+size_t embed_ws_bytes(int Lv, int TXT) {
+    return align256((size_t)Lv * VID_IN_PAD * 2) + align256((size_t)TXT * 5120 * 2);
+}
+size_t final_ws_bytes(int Lv) {
+    return align256(2 * DIM * 4) + align256((size_t)Lv * DIM * 2) + align256((size_t)Lv * VID_OUT_PAD * 4);
+}
+size_t layer_ws_bytes(int M, int mlp) {
+    return align256(12 * DIM * 4) + align256((size_t)M * DIM * 2) + align256((size_t)M * QKV * 2) +
+           align256((size_t)M * DIM * 2) + align256((size_t)M * mlp * 2);
+}
+}  // namespace
+
+int dit_reserve(awa_ctx* ctx, const awa_geom* g, int mlp) {
+    if (!ctx || !g || mlp <= 0 || mlp % 128 != 0) {
+        set_err(ctx, "dit_reserve: bad argument (mlp=%d must be a positive multiple of 128)", mlp);
+        return AWA_EARG;
+    }
+    const int Lv = g->plan.Lv, TXT = g->plan.txt_len;
+    const size_t need = std::max(layer_ws_bytes(Lv + TXT, mlp), std::max(embed_ws_bytes(Lv, TXT), final_ws_bytes(Lv)));
+    DeviceGuard dg(ctx->device);
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, need));
+    return awa_reserve(ctx, g, AWA_BF16);
+}
+
 int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H, int W, const float* d_txt,
               int TXT, float* d_x, awa_stream_t stream) {
     if (!ctx || !io || !d_grid || !d_txt || !d_x || T < 1 || H < 2 || W < 2 || H % 2 || W % 2 || TXT < 1) {
@@ -110,7 +137,7 @@ int dit_embed(awa_ctx* ctx, const dit_io* io, const float* d_grid, int T, int H,
     const int Lv = T * (H / 2) * (W / 2), M = Lv + TXT;
     // workspace: patches [Lv][192] bf16 | text [TXT][5120] bf16
     const size_t o_t = align256((size_t)Lv * VID_IN_PAD * 2);
-    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, o_t + align256((size_t)TXT * 5120 * 2)));
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, embed_ws_bytes(Lv, TXT)));
     uint16_t* patch = static_cast<uint16_t*>(ctx->ws);
     uint16_t* txt = reinterpret_cast<uint16_t*>(static_cast<char*>(ctx->ws) + o_t);
     HIPCK(ctx, launch_patchify(d_grid, T, H, W, patch, VID_IN_PAD, s));
@@ -139,7 +166,7 @@ int dit_final(awa_ctx* ctx, const dit_io* io, const float* d_emb, const float* d
     // workspace: scale, shift [2][2560] f32 | h [Lv][2560] bf16 | y [Lv][256] f32
     const size_t o_h = align256(2 * DIM * 4);
     const size_t o_y = o_h + align256((size_t)Lv * DIM * 2);
-    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, o_y + align256((size_t)Lv * VID_OUT_PAD * 4)));
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, final_ws_bytes(Lv)));
     char* ws = static_cast<char*>(ctx->ws);
     float* scale = reinterpret_cast<float*>(ws);
     float* shift = scale + DIM;
@@ -232,8 +259,7 @@ int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb, con
     const size_t o_qkv = o_h + align256((size_t)M * DIM * 2);
     const size_t o_att = o_qkv + align256((size_t)M * QKV * 2);
     const size_t o_u = o_att + align256((size_t)M * DIM * 2);
-    const size_t need = o_u + align256((size_t)M * mlp * 2);
-    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, need));
+    HIPCK(ctx, ensure_buffer(&ctx->ws, &ctx->ws_bytes, layer_ws_bytes(M, mlp)));
     char* ws = static_cast<char*>(ctx->ws);
     float* ada = reinterpret_cast<float*>(ws);
     uint16_t* h = reinterpret_cast<uint16_t*>(ws + o_h);
