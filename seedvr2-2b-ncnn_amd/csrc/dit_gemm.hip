@@ -45,6 +45,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) void* lptr_t;
 
@@ -134,42 +135,69 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
         }
     } else {  // EPI_RESID, in two halves of 64 features (staged fp32 rows: 256 bytes)
         float* sf = reinterpret_cast<float*>(stg);
+        const int c = lane & 15;
+        // The residual rows of this wave's block through a buffer resource
+        // that ends at row M: rows past it read zeros and their stores are
+        // dropped, so the loop below has no branch per row.  All of a half's
+        // rows are loaded before any is stored: written as load, update,
+        // store per row, every row waited for a full memory round trip
+        // behind the one before (the compiler cannot tell a row's store
+        // from the next row's load apart), 4 MJ of them per half, from HBM
+        // inside the DiT step.
+        // (the fields pass through readfirstlane: a resource the compiler
+        // cannot prove uniform makes it loop over the lanes at every access)
+        const int rows = min(max(p.M - m_base, 0), 16 * MJ);
+        const uint64_t xbase = reinterpret_cast<uint64_t>(reinterpret_cast<float*>(p.C) + (size_t)m_base * p.ldc);
+        // (readfirstlane returns int: each half is taken back to uint32_t
+        // before widening, or a low word with bit 31 set would sign-extend
+        // into the high word)
+        const uint32_t xlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)xbase);
+        const uint32_t xhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(xbase >> 32));
+        const uint64_t xb = ((uint64_t)xhi << 32) | (uint64_t)xlo;
+        const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(xb), 0, __builtin_amdgcn_readfirstlane((uint32_t)rows * p.ldc * 4), 0x00020000);
 #pragma unroll
         for (int half = 0; half < 2; half++) {
+            const int n = n_base + 64 * half + 4 * c;
+            const uint32_t ofs0 = 4u * ((uint32_t)(lane >> 4) * p.ldc + n);  // bytes, row 4 it + lane / 16
+            const uint32_t ofs_it = 16u * p.ldc;
+            float4 xr[4 * MJ];
+#pragma unroll
+            for (int it = 0; it < 4 * MJ; it++) {
+                const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(xres, ofs0 + it * ofs_it, 0, 0);
+                xr[it] = make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                     __uint_as_float(raw[3]));
+            }
 #pragma unroll
             for (int j = 0; j < MJ; j++) {
                 const int r = 16 * j + col;
 #pragma unroll
                 for (int i2 = 0; i2 < 4; i2++) {
                     const f32x4& a = acc[4 * half + i2][j];
-                    const int c = 4 * i2 + q;
-                    *reinterpret_cast<float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2)) =
+                    const int ch = 4 * i2 + q;
+                    *reinterpret_cast<float4*>(sf + r * 64 + ((ch ^ (r & 15)) << 2)) =
                         make_float4(a[0], a[1], a[2], a[3]);
                 }
             }
-            const int c = lane & 15;
-            const int n = n_base + 64 * half + 4 * c;
             float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
             if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n);
             const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);
             const float4 g0 = p.gate0 ? *reinterpret_cast<const float4*>(p.gate0 + n) : one;
             const float4 g1 = p.gate1 ? *reinterpret_cast<const float4*>(p.gate1 + n) : one;
-            float* out = reinterpret_cast<float*>(p.C) + n;
-#pragma unroll 8
+#pragma unroll
             for (int it = 0; it < 4 * MJ; it++) {
                 const int r = 4 * it + (lane >> 4), m = m_base + r;
                 const float4 v = *reinterpret_cast<const float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2));
-                if (m < p.M) {
-                    const float4 gt = m < p.split ? g0 : g1;
-                    float4* dst = reinterpret_cast<float4*>(out + (size_t)m * p.ldc);
-                    float4 x = *dst;
-                    // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
-                    x.x = gt.x * (v.x + b.x) + x.x;
-                    x.y = gt.y * (v.y + b.y) + x.y;
-                    x.z = gt.z * (v.z + b.z) + x.z;
-                    x.w = gt.w * (v.w + b.w) + x.w;
-                    *dst = x;
-                }
+                const float4 gt = m < p.split ? g0 : g1;
+                float4 x = xr[it];
+                // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
+                x.x = gt.x * (v.x + b.x) + x.x;
+                x.y = gt.y * (v.y + b.y) + x.y;
+                x.z = gt.z * (v.z + b.z) + x.z;
+                x.w = gt.w * (v.w + b.w) + x.w;
+                const u32x4 w = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z),
+                                 __float_as_uint(x.w)};
+                __builtin_amdgcn_raw_buffer_store_b128(w, xres, ofs0 + it * ofs_it, 0, 0);
             }
         }
     }
