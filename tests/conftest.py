@@ -77,3 +77,23 @@ def seeded_awa_inputs(Lv, txt, seed, outlier_frac=0.0, outlier_scale=8.0):
             a[m] *= outlier_scale
     gains = [(1.0 + 0.02 * rng.standard_normal(128)).astype(np.float32) for _ in range(4)]
     return vqkv, tqkv, gains
+
+
+def random_shapes(n=24, seed=1234, max_rows=2500):
+    """A seeded list of AWA shapes (t, h, w, num_windows, txt, shifted) with at
+    most max_rows video rows: 1-4 frames, thin and square grids, 1-6 windows
+    per spatial axis and 1-3 in time, 1-140 text rows (around the 64-row
+    tile), both geometries.  The same list drives the planner's CPU stream
+    check and the GPU parity sweep."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        t = int(rng.integers(1, 5))
+        h = int(rng.integers(1, 48))
+        w = int(rng.integers(1, 48))
+        if t * h * w > max_rows or t * h * w < 2:
+            continue
+        nw = (int(rng.integers(1, 4)), int(rng.integers(1, 7)), int(rng.integers(1, 7)))
+        txt = int(rng.choice([1, 2, 31, 58, 63, 64, 65, 77, 128, 140]))
+        out.append((t, h, w, nw, txt, len(out) % 2))
+    return out

@@ -80,3 +80,13 @@ def test_stream_with_empty_window(driver, txt, empty_at):
     64 text rows its work item has one key tile of its own."""
     mk, lpt, mean = run(driver, 1, 23, 27, (4, 3, 3), txt, 0, 16, empty_at)
     assert mk <= lpt and mk >= mean
+
+
+def test_schedule_on_random_shapes(driver):
+    """The seeded random shapes of the GPU parity sweep: every item scheduled
+    once with matching descriptors and every slot's DMA stream replayed
+    (the driver's checks), on the CPU before any of them reaches the device."""
+    from conftest import random_shapes
+    for t, h, w, nw, txt, sh in random_shapes():
+        mk, lpt, mean = run(driver, t, h, w, nw, txt, sh, 512)
+        assert mk <= lpt and mk >= mean, (t, h, w, nw, txt, sh)
