@@ -135,3 +135,12 @@ def test_capi_planner_matches_oracle(oracle, awa, shifted):
         g = oracle.Geometry(*shp, nw, 2, shifted)
         sl = awa.plan_windows(*shp, nw, shifted)
         assert np.array_equal(sl, g.slices), (shp, nw)
+
+
+def test_capi_planner_on_random_shapes(oracle, awa):
+    """The GPU parity sweep's shapes (random_shapes): the C ABI's window plan
+    equals the oracle's before any of them reaches the device."""
+    from conftest import random_shapes
+    for t, h, w, nw, txt, sh in random_shapes():
+        g = oracle.Geometry(t, h, w, nw, txt, sh)
+        assert np.array_equal(awa.plan_windows(t, h, w, nw, sh), g.slices), (t, h, w, nw, txt, sh)
