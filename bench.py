@@ -374,6 +374,69 @@ def gemm_shapes(awa_hip, torch, steps, warmup):
     return {"gemm_shapes": res, "unit": "us per GEMM (HIP events, back-to-back launches, best of 3 alternating rounds)"}
 
 
+def torch_attention(awa_hip, torch, steps, warmup):
+    """PyTorch's fused attention (its flash and memory-efficient backends; the
+    math backend is never used) on exactly the windows of the 1080p layers:
+    every window's S = f + TXT rows attend among themselves, 20 heads of 128,
+    bf16, windows of equal S batched into one call; the same flops as the
+    attention kernel, which is timed beside it (awa_time_phases, back to back)."""
+    import numpy as np
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    ctx = awa_hip.Context(0)
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(SEED)
+    Lv = GRID[0] * GRID[1] * GRID[2]
+    vq = torch.from_numpy(rng.standard_normal((Lv, 7680), dtype=np.float32)).to(dev, torch.bfloat16)
+    tq = torch.from_numpy(rng.standard_normal((TXT, 7680), dtype=np.float32)).to(dev, torch.bfloat16)
+    gains = [torch.from_numpy((1.0 + 0.02 * rng.standard_normal(128)).astype(np.float32)).to(dev)
+             for _ in range(4)]
+    res = {}
+    for sh in (0, 1):
+        g = ctx.build_geometry(*GRID, NUM_WINDOWS, TXT, sh)
+        d = g.read()
+        S = [int(c1 - c0) + TXT for c0, c1 in zip(d["cumf"][:-1], d["cumf"][1:])]
+        fl = sdpa_flops(S)
+        groups = {}
+        for s in S:
+            groups[s] = groups.get(s, 0) + 1
+        gen = torch.Generator(device=dev).manual_seed(sh)
+        ops = [[torch.randn((cnt, 20, s, 128), generator=gen, device=dev).to(torch.bfloat16) for _ in range(3)]
+               for s, cnt in sorted(groups.items())]
+        entry = {"windows": len(S), "window_rows": sorted(groups.items()), "gflop": round(fl / 1e9, 3)}
+        _, attn_ms, _ = ctx.time_phases(g, vq, tq, *gains, reps=steps, eps=1e-5)
+        entry["ours"] = {"us": round(attn_ms * 1e3, 2), "tflops": round(fl / (attn_ms * 1e-3) / 1e12, 1)}
+        for name, be in (("torch_flash", SDPBackend.FLASH_ATTENTION),
+                         ("torch_efficient", SDPBackend.EFFICIENT_ATTENTION)):
+            try:
+                with sdpa_kernel([be]):
+                    def run():
+                        for q, k, v in ops:
+                            F.scaled_dot_product_attention(q, k, v)
+                    for _ in range(warmup):
+                        run()
+                    best = float("inf")
+                    for _ in range(3):
+                        torch.cuda.synchronize()
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(steps):
+                            run()
+                        e1.record()
+                        torch.cuda.synchronize()
+                        best = min(best, e0.elapsed_time(e1) * 1e3 / steps)
+                entry[name] = {"us": round(best, 2), "tflops": round(fl / (best * 1e-6) / 1e12, 1)}
+            except RuntimeError as ex:  # backend not built for this device
+                entry[name] = {"unavailable": str(ex)[:160]}
+        res["shifted" if sh else "unshifted"] = entry
+        g.close()
+    ctx.close()
+    return {"torch_attention": res,
+            "unit": "us per layer's attention (all windows, 20 heads), HIP events over back-to-back launches, "
+                    "torch: best of 3 rounds, one call per group of equal-length windows"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +450,9 @@ def main():
     ap.add_argument("--gemm-shapes", action="store_true",
                     help="only time the DiT block's GEMM kernel and hipBLASLt (torch.mm) on the four "
                          "1080p projection shapes (bf16 in and out), print one JSON line and exit")
+    ap.add_argument("--torch-attention", action="store_true",
+                    help="only time PyTorch's fused attention (flash / memory-efficient backends) on the "
+                         "1080p layers' windows beside the attention kernel, print one JSON line and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run the library's streaming device copy of MB MiB (14 times) to "
                          "calibrate the FETCH_SIZE/WRITE_SIZE counters, then exit")
@@ -421,6 +487,10 @@ def main():
 
     if args.gemm_shapes:
         print(json.dumps(gemm_shapes(awa_hip, torch, args.steps, args.warmup)))
+        return
+
+    if args.torch_attention:
+        print(json.dumps(torch_attention(awa_hip, torch, args.steps, args.warmup)))
         return
 
     dev = torch.device("cuda:0")
