@@ -431,6 +431,29 @@ def torch_attention(awa_hip, torch, steps, warmup):
                 entry[name] = {"unavailable": str(ex)[:160]}
         res["shifted" if sh else "unshifted"] = entry
         g.close()
+    # the same backends on uniform batches (batch, 20 heads, S rows, 128)
+    uni = {}
+    for B, S in ((16, 398), (25, 264), (4, 2048)):
+        gen = torch.Generator(device=dev).manual_seed(S)
+        q, k, v = (torch.randn((B, 20, S, 128), generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
+        fl = 4.0 * B * 20 * S * S * 128
+        for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+            try:
+                with sdpa_kernel([be]):
+                    for _ in range(warmup):
+                        F.scaled_dot_product_attention(q, k, v)
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(steps):
+                        F.scaled_dot_product_attention(q, k, v)
+                    e1.record()
+                    torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / steps
+                uni[f"B{B}_S{S}_{name}"] = {"us": round(us, 1), "tflops": round(fl / (us * 1e-6) / 1e12, 1)}
+            except RuntimeError as ex:
+                uni[f"B{B}_S{S}_{name}"] = {"unavailable": str(ex)[:160]}
+    res["uniform_batches"] = uni
     ctx.close()
     return {"torch_attention": res,
             "unit": "us per layer's attention (all windows, 20 heads), HIP events over back-to-back launches, "
