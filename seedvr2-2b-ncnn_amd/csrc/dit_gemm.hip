@@ -138,12 +138,15 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
         const int c = lane & 15;
         // The residual rows of this wave's block through a buffer resource
         // that ends at row M: rows past it read zeros and their stores are
-        // dropped, so the loop below has no branch per row.  All of a half's
-        // rows are loaded before any is stored: written as load, update,
-        // store per row, every row waited for a full memory round trip
-        // behind the one before (the compiler cannot tell a row's store
-        // from the next row's load apart), 4 MJ of them per half, from HBM
-        // inside the DiT step.
+        // dropped, so there is no branch per row.  Rows go in chunks of 2 MJ
+        // (a quarter of the block's rows and features per lane), each
+        // chunk's loads issued before the chunk ahead of it is updated and
+        // stored: vector memory operations complete in order, so a wait for
+        // a chunk never waits for the stores issued after its loads.
+        // (Written as load, update, store per row, the compiler cannot tell
+        // a row's store from the next row's load apart, and every row waited
+        // a full memory round trip behind the one before, from HBM inside
+        // the DiT step.)
         // (the fields pass through readfirstlane: a resource the compiler
         // cannot prove uniform makes it loop over the lanes at every access)
         const int rows = min(max(p.M - m_base, 0), 16 * MJ);
@@ -156,18 +159,21 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
         const uint64_t xb = ((uint64_t)xhi << 32) | (uint64_t)xlo;
         const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
             reinterpret_cast<void*>(xb), 0, __builtin_amdgcn_readfirstlane((uint32_t)rows * p.ldc * 4), 0x00020000);
+        constexpr int CH = 2 * MJ;  // rows per lane and chunk; chunks (half, part): 4 MJ rows a half
+        const uint32_t ofs_it = 16u * p.ldc;
+        auto ofs0 = [&](int half) __attribute__((always_inline)) {  // bytes, row 4 it + lane / 16
+            return 4u * ((uint32_t)(lane >> 4) * p.ldc + n_base + 64 * half + 4 * c);
+        };
+        auto load_chunk = [&](float4 (&xr)[CH], int half, int part) __attribute__((always_inline)) {
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
-            const int n = n_base + 64 * half + 4 * c;
-            const uint32_t ofs0 = 4u * ((uint32_t)(lane >> 4) * p.ldc + n);  // bytes, row 4 it + lane / 16
-            const uint32_t ofs_it = 16u * p.ldc;
-            float4 xr[4 * MJ];
-#pragma unroll
-            for (int it = 0; it < 4 * MJ; it++) {
-                const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(xres, ofs0 + it * ofs_it, 0, 0);
-                xr[it] = make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
-                                     __uint_as_float(raw[3]));
+            for (int i = 0; i < CH; i++) {
+                const u32x4 raw =
+                    __builtin_amdgcn_raw_buffer_load_b128(xres, ofs0(half) + (part * CH + i) * ofs_it, 0, 0);
+                xr[i] = make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                                    __uint_as_float(raw[3]));
             }
+        };
+        auto stage = [&](int half) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < MJ; j++) {
                 const int r = 16 * j + col;
@@ -179,17 +185,42 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
                         make_float4(a[0], a[1], a[2], a[3]);
                 }
             }
-            float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n);
-            const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);
-            const float4 g0 = p.gate0 ? *reinterpret_cast<const float4*>(p.gate0 + n) : one;
-            const float4 g1 = p.gate1 ? *reinterpret_cast<const float4*>(p.gate1 + n) : one;
+        };
+        // bias and gates of both halves, loaded first and without branches:
+        // a null vector gets an empty resource (its loads read zeros) and
+        // the value is chosen after the load (bias 0, gates 1)
+        auto vec_rsrc = [&](const float* v) __attribute__((always_inline)) {
+            const uint64_t a = reinterpret_cast<uint64_t>(v);
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                                     v ? p.N * 4 : 0, 0x00020000);
+        };
+        auto vec_load = [&](__amdgpu_buffer_rsrc_t r, int n) __attribute__((always_inline)) {
+            const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(r, 4u * n, 0, 0);
+            return make_float4(__uint_as_float(raw[0]), __uint_as_float(raw[1]), __uint_as_float(raw[2]),
+                               __uint_as_float(raw[3]));
+        };
+        const __amdgpu_buffer_rsrc_t bres = vec_rsrc(p.bias), g0res = vec_rsrc(p.gate0), g1res = vec_rsrc(p.gate1);
+        const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);
+        float4 bv[2], g0v[2], g1v[2];
 #pragma unroll
-            for (int it = 0; it < 4 * MJ; it++) {
+        for (int half = 0; half < 2; half++) {
+            const int n = n_base + 64 * half + 4 * c;
+            bv[half] = vec_load(bres, n);
+            const float4 l0 = vec_load(g0res, n), l1 = vec_load(g1res, n);
+            g0v[half] = p.gate0 ? l0 : one;
+            g1v[half] = p.gate1 ? l1 : one;
+        }
+        auto update = [&](const float4 (&xr)[CH], int half, int part) __attribute__((always_inline)) {
+            const float4 b = bv[half], g0 = g0v[half], g1 = g1v[half];
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const int it = part * CH + i;
                 const int r = 4 * it + (lane >> 4), m = m_base + r;
                 const float4 v = *reinterpret_cast<const float4*>(sf + r * 64 + ((c ^ (r & 15)) << 2));
                 const float4 gt = m < p.split ? g0 : g1;
-                float4 x = xr[it];
+                float4 x = xr[i];
                 // gate * (proj + bias), then the residual add (dit_vk.cpp:558-575)
                 x.x = gt.x * (v.x + b.x) + x.x;
                 x.y = gt.y * (v.y + b.y) + x.y;
@@ -197,9 +228,20 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
                 x.w = gt.w * (v.w + b.w) + x.w;
                 const u32x4 w = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z),
                                  __float_as_uint(x.w)};
-                __builtin_amdgcn_raw_buffer_store_b128(w, xres, ofs0 + it * ofs_it, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(w, xres, ofs0(half) + it * ofs_it, 0, 0);
             }
-        }
+        };
+        float4 xa[CH], xc[CH];
+        load_chunk(xa, 0, 0);
+        stage(0);
+        load_chunk(xc, 0, 1);
+        update(xa, 0, 0);
+        load_chunk(xa, 1, 0);
+        update(xc, 0, 1);
+        stage(1);  // after the last reads of half 0's staged rows (same wave, LDS in order)
+        load_chunk(xc, 1, 1);
+        update(xa, 1, 0);
+        update(xc, 1, 1);
     }
 }
 
