@@ -38,6 +38,13 @@ extern "C" {
 
 enum { DIT_MLP = 6912, DIT_EMB = 15360 };
 
+/* Size limits of the block's GEMM kernel: its operand and output rows are
+ * addressed through buffer resources with 32-bit byte ranges over a tile's
+ * rows, so N and K stay at or under 2^20 and the MLP width (N of the fused
+ * SwiGLU GEMM is twice it) at or under 2^19; larger values are rejected
+ * (AWA_EARG).  The model's widths are 2560, 7680 and 6912. */
+enum { DIT_GEMM_NK_MAX = 1 << 20, DIT_MLP_MAX = 1 << 19 };
+
 /* One branch's weights on the device (names as the reference's per-branch
  * files, dit_vk.cpp:163-177 and verify_dit.cpp:163-179). */
 typedef struct {
@@ -158,7 +165,7 @@ int dit_forward_grid(awa_ctx* ctx, const dit_io* io, const dit_time_weights* tw,
 
 /* Plain bf16 GEMM with the block's kernel, for tests and measurement:
  * C[M][N] = A[M][K] W[N][K]^T, bf16 in, bf16 out (fp32 accumulation).
- * N a multiple of 256, K a multiple of 64. */
+ * N a multiple of 256, K a multiple of 64, both at most DIT_GEMM_NK_MAX. */
 int dit_gemm_bf16(awa_ctx* ctx, const uint16_t* d_A, const uint16_t* d_W, uint16_t* d_C, int M,
                   int N, int K, awa_stream_t stream);
 

@@ -115,8 +115,9 @@ size_t layer_ws_bytes(int M, int mlp) {
 }  // namespace
 
 int dit_reserve(awa_ctx* ctx, const awa_geom* g, int mlp) {
-    if (!ctx || !g || mlp <= 0 || mlp % 128 != 0) {
-        set_err(ctx, "dit_reserve: bad argument (mlp=%d must be a positive multiple of 128)", mlp);
+    if (!ctx || !g || mlp <= 0 || mlp % 128 != 0 || mlp > DIT_MLP_MAX) {
+        set_err(ctx, "dit_reserve: bad argument (mlp=%d must be a positive multiple of 128, at most %d)", mlp,
+                DIT_MLP_MAX);
         return AWA_EARG;
     }
     const int Lv = g->plan.Lv, TXT = g->plan.txt_len;
@@ -189,8 +190,9 @@ int dit_final(awa_ctx* ctx, const dit_io* io, const float* d_emb, const float* d
 
 int dit_pack_mlp_weights(awa_ctx* ctx, const uint16_t* d_w_in, const uint16_t* d_w_gate, int mlp,
                          uint16_t* d_w_cat, awa_stream_t stream) {
-    if (!ctx || !d_w_in || !d_w_gate || !d_w_cat || mlp <= 0 || mlp % 128 != 0) {
-        set_err(ctx, "dit_pack_mlp_weights: bad argument (mlp=%d must be a positive multiple of 128)", mlp);
+    if (!ctx || !d_w_in || !d_w_gate || !d_w_cat || mlp <= 0 || mlp % 128 != 0 || mlp > DIT_MLP_MAX) {
+        set_err(ctx, "dit_pack_mlp_weights: bad argument (mlp=%d must be a positive multiple of 128, at most %d)",
+                mlp, DIT_MLP_MAX);
         return AWA_EARG;
     }
     DeviceGuard dg(ctx->device);
@@ -220,8 +222,10 @@ int dit_time_embedding(awa_ctx* ctx, float t, const float* d_w_in, const float* 
 
 int dit_gemm_bf16(awa_ctx* ctx, const uint16_t* d_A, const uint16_t* d_W, uint16_t* d_C, int M, int N,
                   int K, awa_stream_t stream) {
-    if (!ctx || !d_A || !d_W || !d_C || M < 1 || N < 256 || N % 256 || K < 64 || K % 64) {
-        set_err(ctx, "dit_gemm_bf16: bad argument M=%d N=%d K=%d (N %% 256 == 0, K %% 64 == 0)", M, N, K);
+    if (!ctx || !d_A || !d_W || !d_C || M < 1 || N < 256 || N % 256 || N > DIT_GEMM_NK_MAX || K < 64 || K % 64 ||
+        K > DIT_GEMM_NK_MAX) {
+        set_err(ctx, "dit_gemm_bf16: bad argument M=%d N=%d K=%d (N %% 256 == 0, K %% 64 == 0, N, K <= %d)", M, N, K,
+                DIT_GEMM_NK_MAX);
         return AWA_EARG;
     }
     DeviceGuard dg(ctx->device);
@@ -244,8 +248,9 @@ int dit_layer_forward(awa_ctx* ctx, const awa_geom* g, const dit_branch* vb, con
                 TXT, g->plan.Lv, g->plan.txt_len);
         return AWA_EARG;
     }
-    if (mlp <= 0 || mlp % 128 != 0 || !(eps > 0.f)) {
-        set_err(ctx, "dit_layer_forward: mlp=%d must be a positive multiple of 128, eps > 0", mlp);
+    if (mlp <= 0 || mlp % 128 != 0 || mlp > DIT_MLP_MAX || !(eps > 0.f)) {
+        set_err(ctx, "dit_layer_forward: mlp=%d must be a positive multiple of 128 (at most %d), eps > 0", mlp,
+                DIT_MLP_MAX);
         return AWA_EARG;
     }
     DeviceGuard dg(ctx->device);

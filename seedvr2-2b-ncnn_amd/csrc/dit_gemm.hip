@@ -60,6 +60,20 @@ constexpr int STAGE_E = (BN + BM) * ROW_E;
 __device__ inline int swz(int row, int chunk) { return row * ROW_E + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 
+// A buffer resource over `bytes` from p with wave-uniform fields
+// (readfirstlane returns int: each half of the address is taken back to
+// uint32_t before widening, or a low word with bit 31 set would sign-extend
+// into the high word; a resource the compiler cannot prove uniform makes it
+// loop over the lanes at every access).  Loads past `bytes` read zeros and
+// stores past it are dropped.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
+}
+
 // Epilogues go through LDS so that global memory sees whole rows: stores of
 // 8- or 16-byte pieces of 32 rows per instruction (the accumulator layout)
 // cost the memory system several times what whole 128-byte lines do.  Each
@@ -89,13 +103,25 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
                 *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ (r & 15)) << 3) + 4 * (q & 1)) = u;
             }
         }
+        // read back MJ staged rows per lane at a time, then store them
+        // through a resource that ends at row M (no branch per row, so the
+        // reads are not each waited for before their store)
         const int c = lane & 15;
-        uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + n_base + c * 8;
-#pragma unroll 8
-        for (int it = 0; it < 4 * MJ; it++) {
-            const int r = 4 * it + (lane >> 4), m = m_base + r;
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 128 + ((c ^ (r & 15)) << 3));
-            if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
+        const __amdgpu_buffer_rsrc_t cres = uniform_rsrc(
+            reinterpret_cast<uint16_t*>(p.C) + (size_t)m_base * p.ldc,
+            (uint32_t)min(max(p.M - m_base, 0), 16 * MJ) * p.ldc * 2);
+        const uint32_t ofs0 = 2u * ((uint32_t)(lane >> 4) * p.ldc + n_base + c * 8);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            u32x4 v[MJ];
+#pragma unroll
+            for (int k = 0; k < MJ; k++) {
+                const int r = 4 * (g * MJ + k) + (lane >> 4);
+                v[k] = *reinterpret_cast<const u32x4*>(stg + r * 128 + ((c ^ (r & 15)) << 3));
+            }
+#pragma unroll
+            for (int k = 0; k < MJ; k++)
+                __builtin_amdgcn_raw_buffer_store_b128(v[k], cres, ofs0 + (g * MJ + k) * 8u * p.ldc, 0, 0);
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
         // W rows alternate 32 in / 32 gate: blocks (4h + e, 4h + 2 + e) are
@@ -125,13 +151,24 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
                         make_uint2(packed[0], packed[1]);
                 }
         }
+        // read back MJ staged rows per lane at a time, then store them
+        // through a resource that ends at row M (as in EPI_STORE)
         const int c = lane & 7;
-        uint16_t* out = reinterpret_cast<uint16_t*>(p.C) + (n_base >> 1) + c * 8;
-#pragma unroll 8
-        for (int it = 0; it < 2 * MJ; it++) {
-            const int r = 8 * it + (lane >> 3), m = m_base + r;
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3));
-            if (m < p.M) *reinterpret_cast<uint4*>(out + (size_t)m * p.ldc) = v;
+        const __amdgpu_buffer_rsrc_t cres = uniform_rsrc(
+            reinterpret_cast<uint16_t*>(p.C) + (size_t)m_base * p.ldc,
+            (uint32_t)min(max(p.M - m_base, 0), 16 * MJ) * p.ldc * 2);
+        const uint32_t ofs0 = 2u * ((uint32_t)(lane >> 3) * p.ldc + (n_base >> 1) + c * 8);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            u32x4 v[MJ];
+#pragma unroll
+            for (int k = 0; k < MJ; k++) {
+                const int r = 8 * (g * MJ + k) + (lane >> 3);
+                v[k] = *reinterpret_cast<const u32x4*>(stg + r * 64 + ((c ^ ((r >> 1) & 7)) << 3));
+            }
+#pragma unroll
+            for (int k = 0; k < MJ; k++)
+                __builtin_amdgcn_raw_buffer_store_b128(v[k], cres, ofs0 + (g * MJ + k) * 16u * p.ldc, 0, 0);
         }
     } else {  // EPI_RESID, in two halves of 64 features (staged fp32 rows: 256 bytes)
         float* sf = reinterpret_cast<float*>(stg);
@@ -147,18 +184,8 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
         // a row's store from the next row's load apart, and every row waited
         // a full memory round trip behind the one before, from HBM inside
         // the DiT step.)
-        // (the fields pass through readfirstlane: a resource the compiler
-        // cannot prove uniform makes it loop over the lanes at every access)
-        const int rows = min(max(p.M - m_base, 0), 16 * MJ);
-        const uint64_t xbase = reinterpret_cast<uint64_t>(reinterpret_cast<float*>(p.C) + (size_t)m_base * p.ldc);
-        // (readfirstlane returns int: each half is taken back to uint32_t
-        // before widening, or a low word with bit 31 set would sign-extend
-        // into the high word)
-        const uint32_t xlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)xbase);
-        const uint32_t xhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(xbase >> 32));
-        const uint64_t xb = ((uint64_t)xhi << 32) | (uint64_t)xlo;
-        const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<void*>(xb), 0, __builtin_amdgcn_readfirstlane((uint32_t)rows * p.ldc * 4), 0x00020000);
+        const __amdgpu_buffer_rsrc_t xres = uniform_rsrc(reinterpret_cast<float*>(p.C) + (size_t)m_base * p.ldc,
+                                                        (uint32_t)min(max(p.M - m_base, 0), 16 * MJ) * p.ldc * 4);
         constexpr int CH = 2 * MJ;  // rows per lane and chunk; chunks (half, part): 4 MJ rows a half
         const uint32_t ofs_it = 16u * p.ldc;
         auto ofs0 = [&](int half) __attribute__((always_inline)) {  // bytes, row 4 it + lane / 16
@@ -190,11 +217,7 @@ __device__ inline void epilogue(const GemmProblem& p, const f32x4 (&acc)[8][MJ],
         // a null vector gets an empty resource (its loads read zeros) and
         // the value is chosen after the load (bias 0, gates 1)
         auto vec_rsrc = [&](const float* v) __attribute__((always_inline)) {
-            const uint64_t a = reinterpret_cast<uint64_t>(v);
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
-                                                     v ? p.N * 4 : 0, 0x00020000);
+            return uniform_rsrc(v, v ? p.N * 4 : 0);
         };
         auto vec_load = [&](__amdgpu_buffer_rsrc_t r, int n) __attribute__((always_inline)) {
             const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(r, 4u * n, 0, 0);

@@ -46,6 +46,17 @@ def test_gemm_rejects_bad_shapes(ctx, awa):
     W = torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(awa.AwaError):
         ctx.gemm(A, W)
+    # N or K above the kernel's 32-bit resource ranges (2^20): rejected
+    # before any device work (the shapes are not backed by the buffers)
+    import ctypes as C
+    for n, k in (((1 << 20) + 256, 64), (256, (1 << 20) + 64)):
+        rc = awa.lib().dit_gemm_bf16(ctx.ptr, C.c_void_p(A.data_ptr()), C.c_void_p(W.data_ptr()),
+                                     C.c_void_p(A.data_ptr()), 8, n, k, None)
+        assert rc != 0, (n, k)
+    g = ctx.build_geometry(1, 4, 4, (1, 1, 1), 3, 0)
+    with pytest.raises(awa.AwaError):
+        ctx.dit_reserve(g, (1 << 19) + 128)
+    g.close()
 
 
 def test_time_embedding(oracle, ctx):
