@@ -76,17 +76,25 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, size_t
     for (size_t j = i; j < n16; j += stride) p[j] = make_uint4(0, 0, 0, 0);
 }
 
-// Streaming device copy: four 16-byte loads per thread in flight, then four
-// nontemporal stores.  The variant that moved bytes fastest among 1, 4, 8 and
-// 16 loads per thread, plain or nontemporal loads and stores, one-shot or
-// grid-stride grids (56 MiB to 1 GiB): it sets the HBM ceiling that the
-// memory-bound passes are compared with.
+// Streaming device copy: CP_U 16-byte loads per thread in flight, then CP_U
+// nontemporal stores; it sets the HBM ceiling that the memory-bound passes
+// are compared with.  Whole blocks take a path with no bounds test, so the
+// loads are issued together and waited for once (with a test per load the
+// compiler waited for each load before the next); only the last block tests.
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int CP_U = 4;
 __global__ __launch_bounds__(256) void stream_copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
                                                           size_t n16) {
-    const size_t base = (size_t)blockIdx.x * CP_U * 256 + threadIdx.x;
+    const size_t block0 = (size_t)blockIdx.x * CP_U * 256;
+    const size_t base = block0 + threadIdx.x;
     u32x4 v[CP_U];
+    if (block0 + CP_U * 256 <= n16) {
+#pragma unroll
+        for (int u = 0; u < CP_U; u++) v[u] = src[base + (size_t)u * 256];
+#pragma unroll
+        for (int u = 0; u < CP_U; u++) __builtin_nontemporal_store(v[u], dst + base + (size_t)u * 256);
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < CP_U; u++) {
         const size_t i = base + (size_t)u * 256;
