@@ -749,8 +749,8 @@ def main():
         if not args.no_mlp10240:
             out["dit_step_mlp10240"] = dit_step(ctx, awa_hip, torch, max(2, args.dit_steps // 2), 1, mlp=10240,
                                                 graph=False)
-            out["dit_step_mlp10240"]["label"] = ("BASELINE config 3 as written (MLP 2560->10240->2560); the "
-                                                 "reference checkpoint's width is 6912 (dit_step)")
+            out["dit_step_mlp10240"]["label"] = ("the DiT-step workload with the MLP written as 2560->10240->2560; "
+                                                 "the reference checkpoint's width is 6912 (dit_step)")
     if not args.no_cpu_baseline:
         vqf = vq.float().cpu().numpy()
         tqf = tq.float().cpu().numpy()

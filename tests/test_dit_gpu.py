@@ -107,9 +107,9 @@ def test_layer_small(oracle, ctx, kind, shifted):
 @pytest.mark.parametrize("kind,mlp", [("shared", 6912), ("dual", 6912), ("shared", 10240)])
 def test_layer_1080p(oracle, ctx, kind, mlp):
     """One full-size layer (1x68x80 grid, TXT 58), odd (shifted) geometry, at the
-    reference checkpoint's MLP width 6912 (dit_vk.cpp:19) and at the 10240 of
-    the DiT-step workload as BASELINE's config 3 writes it (timed by bench.py
-    as the MLP-10240 step)."""
+    reference checkpoint's MLP width 6912 (dit_vk.cpp:19) and at 10240, the MLP
+    width of the 1080p DiT-step workload's stated shape (timed by bench.py as
+    the MLP-10240 step)."""
     note(f"layer 1080p {kind} mlp={mlp}")
     x, out, ref, Lv = run_layer(oracle, ctx, (1, 68, 80), (4, 3, 3), 58, 1, mlp, kind, 50)
     for sl in (slice(0, Lv), slice(Lv, None)):
