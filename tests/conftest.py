@@ -79,12 +79,15 @@ def seeded_awa_inputs(Lv, txt, seed, outlier_frac=0.0, outlier_scale=8.0):
     return vqkv, tqkv, gains
 
 
-def random_shapes(n=24, seed=1234, max_rows=2500):
+def random_shapes(n=None, seed=None, max_rows=2500):
     """A seeded list of AWA shapes (t, h, w, num_windows, txt, shifted) with at
     most max_rows video rows: 1-4 frames, thin and square grids, 1-6 windows
     per spatial axis and 1-3 in time, 1-140 text rows (around the 64-row
     tile), both geometries.  The same list drives the planner's CPU stream
-    check and the GPU parity sweep."""
+    check and the GPU parity sweep; AWA_SWEEP_N and AWA_SWEEP_SEED (default
+    24 shapes, seed 1234) widen or move it for a run of both."""
+    n = int(os.environ.get("AWA_SWEEP_N", 24)) if n is None else n
+    seed = int(os.environ.get("AWA_SWEEP_SEED", 1234)) if seed is None else seed
     rng = np.random.default_rng(seed)
     out = []
     while len(out) < n:

@@ -1,7 +1,8 @@
 """GPU parity on a seeded sweep of random AWA shapes (tests/conftest.py
 random_shapes: 1-4 latent frames, thin and square grids up to 2,500 video rows,
 1-3 windows in time and 1-6 per spatial axis, 1-140 text rows, both
-geometries), through the C ABI against the oracle:
+geometries; inputs N(0, 1) with 1 % of the values x8), through the C ABI against
+the oracle (AWA_SWEEP_N / AWA_SWEEP_SEED widen or move the sweep):
   - the device geometry (slices, cumf, vidx, RoPE tables): bit-exact;
   - bf16 storage: cos >= 0.9999 against the reference bf16 path (bf16 inputs
     widened exactly, fp32 attention, outputs rounded to nearest even);
@@ -40,7 +41,7 @@ def test_random_shape(oracle, ctx, k):
     assert np.array_equal(d["vidx"], o.vidx)
     assert np.array_equal(d["vid_freq"].view(np.uint32), o.vid_freq.view(np.uint32))
     assert np.array_equal(d["txt_freq"].view(np.uint32), o.txt_freq.view(np.uint32))
-    vq, tq, gains = seeded_awa_inputs(o.Lv, txt, 100 + k)
+    vq, tq, gains = seeded_awa_inputs(o.Lv, txt, 100 + k, outlier_frac=0.01)
     g4 = [torch.from_numpy(x).to(dev) for x in gains]
     rv, rt = oracle.awa_forward(oracle.bf16_round(vq), oracle.bf16_round(tq), o, *gains, eps=1e-5)
     refs = {"bf16": (oracle.bf16_round(rv), oracle.bf16_round(rt))}
