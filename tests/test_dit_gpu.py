@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import metrics
+from conftest import metrics, random_shapes
 from dit_reference import layer_emulation, random_branch, random_emb, to_device
 
 pytestmark = pytest.mark.gpu
@@ -101,6 +101,28 @@ def test_layer_small(oracle, ctx, kind, shifted):
         cos, rel, _ = metrics(out[sl], ref[sl])
         dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
         note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
+        assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
+
+
+LAYER_SHAPES = random_shapes(6, seed=77, max_rows=700)
+
+
+@pytest.mark.parametrize("k", range(len(LAYER_SHAPES)))
+def test_layer_random_shapes(oracle, ctx, k):
+    """Whole layers on seeded random shapes (random_shapes, up to 700 video rows
+    and 1-140 text rows), the three kinds in turn: the block's GEMMs see row
+    counts M = Lv + TXT (and the branches' Lv and TXT) at many offsets within
+    their 224- and 256-row tiles, which their epilogues bound through buffer
+    resources."""
+    t, h, w, nw, txt, sh = LAYER_SHAPES[k]
+    kind = ("shared", "dual", "last")[k % 3]
+    note(f"layer random shape {k}: grid ({t},{h},{w}) windows {nw} txt {txt} shifted {sh} {kind}")
+    x, out, ref, Lv = run_layer(oracle, ctx, (t, h, w), nw, txt, sh, 256, kind, 70 + k)
+    for sl in (slice(0, Lv), slice(Lv, None)):
+        cos, rel, _ = metrics(out[sl], ref[sl])
+        dcos, drel, _ = metrics(out[sl] - x[sl], ref[sl] - x[sl])
+        note(f"  cos={cos:.8f} update cos={dcos:.7f} rel={drel:.2e}")
+        assert np.all(np.isfinite(out[sl]))
         assert cos >= BF16_COS and dcos >= 0.999, (cos, dcos)
 
 
